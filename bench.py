@@ -1,0 +1,304 @@
+"""Paged-KV decode benchmark on one MI355X.
+
+A step is one decode step of the paged-KV path over one batch: split-context
+paged decode attention (partition kernel + log-sum-exp reduce) over every
+request's context, followed by a one-token KV append per request — the
+order of the reference's decode step (decode.py:480-487).
+
+Default workload (the GQA decode shape): batch 32, 32 query heads / 8 KV
+heads, head_dim 128, bf16, block size 16, ragged context lengths uniform in
+[4096, 8192] (seeded), block tables drawn by random permutation from a pool
+of 20,000 physical blocks, K/V/q ~ N(0,1), 512-token partitions. Inputs are
+resident in HBM before the timed region.
+
+Prints ONE JSON line. ``value`` is the algorithmic HBM bytes of a step
+divided by its wall time (GB/s); ``roofline`` times the attention partition
+kernel with HIP events recorded around it on its stream; ``cpu_baseline``
+times the CPU oracle (a numpy restatement of paged_reference) on a bounded
+sample of the same requests.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+PEAK_HBM_GBPS = 8000.0
+METRIC = "paged decode attn µs/step + HBM GB/s (% peak), GQA 32/8 hd128 bf16"
+
+WORKLOADS = {
+    # name: (batch, heads, kv_heads, head_dim, dtype, ctx_lo, ctx_hi, pool, kv_scale, partition)
+    "gqa32x8_hd128_bf16_b32_ctx4k-8k": (32, 32, 8, 128, torch.bfloat16, 4096, 8192, 20000, 1.0, 512),
+    "mha32_hd128_fp16_b16_ctx512": (16, 32, 32, 128, torch.float16, 512, 512, None, 1.0, None),
+    "mqa32x1_hd128_bf16_b64_ctx1k-4k": (64, 32, 1, 128, torch.bfloat16, 1024, 4096, None, 0.5, None),
+}
+DEFAULT_WORKLOAD = "gqa32x8_hd128_bf16_b32_ctx4k-8k"
+
+
+class HipEvents:
+    """Raw hipEvent_t handles from the HIP runtime torch already loaded."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so.7")
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self) -> int:
+        handle = ctypes.c_void_p()
+        rc = self.lib.hipEventCreate(ctypes.byref(handle))
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreate failed: {rc}")
+        return handle.value
+
+    def elapsed_ms(self, start: int, end: int) -> float:
+        out = ctypes.c_float()
+        rc = self.lib.hipEventElapsedTime(ctypes.byref(out), ctypes.c_void_p(start), ctypes.c_void_p(end))
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed: {rc}")
+        return float(out.value)
+
+    def destroy(self, handle: int) -> None:
+        self.lib.hipEventDestroy(ctypes.c_void_p(handle))
+
+
+def build_workload(name: str, device: torch.device, seed: int = 0):
+    from inferkernellab_amd import PagedKVCache
+
+    batch, heads, kv_heads, head_dim, dtype, lo, hi, pool, kv_scale, _ = WORKLOADS[name]
+    block_size = 16
+    gen = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(lo, hi + 1, (batch,), generator=gen).tolist()
+    need = [-(-(n + 1) // block_size) for n in lengths]  # room for the appended token
+    pool = pool or sum(need) + 8
+    perm = torch.randperm(pool, generator=gen).tolist()
+    tables, used = [], 0
+    for n in need:
+        tables.append(perm[used : used + n])
+        used += n
+    width = max(need)
+    padded = [t + [0] * (width - len(t)) for t in tables]
+    cache = PagedKVCache(pool, block_size, kv_heads, head_dim, dtype=dtype, device=device)
+    dgen = torch.Generator(device=device).manual_seed(seed + 1)
+    for t in (cache.k, cache.v):
+        t.normal_(0.0, kv_scale, generator=dgen)
+    query = torch.randn(batch, heads, head_dim, generator=dgen, device=device, dtype=torch.float32).to(dtype)
+    new_k = (torch.randn(batch, kv_heads, head_dim, generator=dgen, device=device) * kv_scale).to(dtype)
+    new_v = (torch.randn(batch, kv_heads, head_dim, generator=dgen, device=device) * kv_scale).to(dtype)
+    slots = [tables[b][n // block_size] * block_size + n % block_size for b, n in enumerate(lengths)]
+    return {
+        "cache": cache,
+        "query": query,
+        "tables": torch.tensor(padded, dtype=torch.int32, device=device),
+        "tables_list": tables,
+        "lengths": lengths,
+        "lens": torch.tensor(lengths, dtype=torch.int32, device=device),
+        "new_k": new_k,
+        "new_v": new_v,
+        "slots": torch.tensor(slots, dtype=torch.int32, device=device),
+        "dtype": dtype,
+        "heads": heads,
+        "kv_heads": kv_heads,
+        "head_dim": head_dim,
+        "block_size": block_size,
+        "pool": pool,
+    }
+
+
+def attention_bytes(lengths, heads: int, kv_heads: int, head_dim: int, elem_bytes: int,
+                    block_size: int, idx_bytes: int = 4) -> int:
+    """Algorithmic HBM bytes of one paged decode attention launch: the K+V
+    rows of every context token (the reference's estimated_kv_read_bytes,
+    benchmark.py:271-278, summed over ragged lengths), the q and out rows,
+    the block-table entries and the context lengths read."""
+    kv = sum(lengths) * kv_heads * head_dim * 2 * elem_bytes
+    q_out = 2 * len(lengths) * heads * head_dim * elem_bytes
+    table = sum(-(-n // block_size) for n in lengths) * idx_bytes
+    return kv + q_out + table + len(lengths) * idx_bytes
+
+
+def step_bytes(w) -> tuple[int, int]:
+    """(attention algorithmic bytes, append algorithmic bytes) of one step."""
+    eb = torch.tensor([], dtype=w["dtype"]).element_size()
+    attn = attention_bytes(w["lengths"], w["heads"], w["kv_heads"], w["head_dim"], eb, w["block_size"])
+    batch = len(w["lengths"])
+    append = 2 * 2 * batch * w["kv_heads"] * w["head_dim"] * eb + batch * 4  # K,V read + write, slots
+    return attn, append
+
+
+def cpu_baseline(w, budget_s: float) -> dict:
+    """Times the CPU oracle (numpy paged_reference) on the first requests of
+    the same workload until ~budget_s of CPU work, then scales to one step."""
+    import numpy as np
+    from oracle import paged_oracle as po
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([info.get("num_threads", 1) for info in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    cache = w["cache"]
+    dtype = {torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32"}[w["dtype"]]
+    oc = po.OracleCache.__new__(po.OracleCache)
+    oc.num_layers, oc.num_blocks, oc.block_size = 1, w["pool"], w["block_size"]
+    oc.num_kv_heads, oc.head_dim, oc.dtype = w["kv_heads"], w["head_dim"], dtype
+
+    def host(t):
+        t = t.detach().cpu()
+        return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
+
+    oc.k, oc.v = host(cache.k), host(cache.v)
+    q = po.to_f32(host(w["query"]), dtype)
+    done, elapsed, kv_bytes = 0, 0.0, 0
+    eb = cache.k.element_size()
+    while done < len(w["lengths"]) and elapsed < budget_s:
+        b = done
+        t0 = time.perf_counter()
+        po.paged_decode_attention(q[b : b + 1], oc, [w["tables_list"][b]], [w["lengths"][b]])
+        elapsed += time.perf_counter() - t0
+        kv_bytes += w["lengths"][b] * w["kv_heads"] * w["head_dim"] * 2 * eb
+        done += 1
+    per_request_s = elapsed / done
+    step_s = per_request_s * len(w["lengths"])
+    return {
+        "value": round(step_s * 1e6, 1),
+        "unit": "us/step",
+        "gbps": round(kv_bytes / elapsed / 1e9, 3),
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle paged_reference (numpy fp32) on the first {done} of {len(w['lengths'])} "
+                  f"requests ({elapsed:.1f} s), scaled to the full batch",
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
+    parser.add_argument("--partition-size", type=int, default=None)
+    parser.add_argument("--cpu-budget-s", type=float, default=15.0)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--seed", type=int, default=0)
+    args = parser.parse_args()
+
+    if args.gpus != 1:
+        print(json.dumps({"error": "this benchmark runs on exactly one GPU: the paged decode path "
+                                   "is measured on one GPU's share; --gpus must be 1"}))
+        return 2
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        return 2
+
+    from inferkernellab_amd import ops
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    w = build_workload(args.workload, device, args.seed)
+    partition = args.partition_size or WORKLOADS[args.workload][9]
+    attn = ops.PreparedPagedAttention(
+        w["query"], w["cache"], w["tables"], w["lens"], validate_inputs=True,
+        partition_size=partition, max_context_len=max(w["lengths"]),
+    )
+    append = ops.PreparedAppend(w["new_k"], w["new_v"], w["cache"], w["slots"])
+    events = HipEvents()
+    k_steps, warmup = args.steps, args.warmup
+    ev = [[events.create() for _ in range(3)] for _ in range(k_steps)]
+
+    for _ in range(warmup):
+        attn()
+        append()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(k_steps):
+        attn(events=ev[i])
+        append()
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    kernel_ms = [events.elapsed_ms(e[0], e[1]) for e in ev]
+    reduce_ms = [events.elapsed_ms(e[1], e[2]) for e in ev]
+    for trio in ev:
+        for h in trio:
+            events.destroy(h)
+
+    attn_bytes, append_bytes = step_bytes(w)
+    ms_per_step = wall_s * 1e3 / k_steps
+    step_gbps = (attn_bytes + append_bytes) / (ms_per_step * 1e-3) / 1e9
+    kern_avg_ms = sum(kernel_ms) / len(kernel_ms)
+    # Algorithmic bytes of the partition kernel: K/V + q + tables + lengths
+    # (+ its fp32 partial writes are workspace traffic, not algorithmic).
+    achieved = attn_bytes / (kern_avg_ms * 1e-3) / 1e9
+
+    traffic = None
+    traffic_file = ROOT / "profiles" / f"traffic_{args.workload}.json"
+    if traffic_file.exists():
+        try:
+            traffic = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(w, args.cpu_budget_s)
+
+    record = {
+        "metric": METRIC,
+        "value": round(step_gbps, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": k_steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "us_per_step": round(ms_per_step * 1e3, 1),
+        "pct_of_peak_hbm": round(100 * step_gbps / PEAK_HBM_GBPS, 1),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[w["dtype"]],
+        "data": "synthetic (seeded N(0,1) K/V/q, random-permutation block tables)",
+        "config": {
+            "workload": args.workload,
+            "batch": len(w["lengths"]),
+            "num_heads": w["heads"],
+            "num_kv_heads": w["kv_heads"],
+            "head_dim": w["head_dim"],
+            "block_size": w["block_size"],
+            "num_blocks": w["pool"],
+            "context_tokens": sum(w["lengths"]),
+            "partition_size": attn.partition_size,
+            "step": "paged attention (partition + reduce) then 1-token KV append per request",
+            "parallelism": "single GPU",
+        },
+        "attention_kernel_us": round(kern_avg_ms * 1e3, 2),
+        "reduce_kernel_us": round(sum(reduce_ms) / len(reduce_ms) * 1e3, 2),
+        "algorithmic_bytes_per_step": attn_bytes + append_bytes,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "traffic": traffic,
+            "kernel": "paged_decode_scalar_kernel",
+            "algorithmic_bytes_per_launch": attn_bytes,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(record))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

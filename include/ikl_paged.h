@@ -1,0 +1,169 @@
+/*
+ * ikl_paged.h — C ABI of the MI355X (gfx950) paged-KV decode library
+ * (libikl_paged.so).
+ *
+ * The library holds two hot operations of paged-KV decoding:
+ *   - KV append: scatter new K/V rows into physical cache slots;
+ *   - paged decode attention for MHA / GQA / MQA over a block-table
+ *     addressed cache, with optional split-context partitions and a
+ *     log-sum-exp reduce kernel.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer (HBM) except the argument structs
+ *     themselves, which live in host memory and are read during the call.
+ *   - Strides are in ELEMENTS of the tensor they describe, not bytes.
+ *   - The cache layout is the reference's [layers, blocks, block_size,
+ *     kv_heads, head_dim]; callers pass the base pointer of ONE layer
+ *     (cache.k[layer], cache.v[layer]) plus its block/token/head strides.
+ *   - The last dimension (head_dim) of every tensor is contiguous.
+ *   - All work is enqueued on `stream` (a hipStream_t, NULL = default
+ *     stream). No call synchronises the host, allocates device memory or
+ *     keeps device state between calls.
+ *   - Return value: 0 on success, a negative IKL_E* code otherwise; the
+ *     message of the last failure on the calling thread is returned by
+ *     ikl_last_error().
+ */
+#ifndef IKL_PAGED_H
+#define IKL_PAGED_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of query / cache / key / value / output tensors. */
+enum ikl_dtype {
+  IKL_F16 = 0,
+  IKL_BF16 = 1,
+  IKL_F32 = 2,
+};
+
+/* Element types of index tensors (slots, block tables, context lengths). */
+enum ikl_index_type {
+  IKL_I32 = 0,
+  IKL_I64 = 1,
+};
+
+/* Status codes. */
+enum ikl_status {
+  IKL_OK = 0,
+  IKL_EINVAL = -1,      /* bad argument (shape, stride, alignment, dtype) */
+  IKL_EUNSUPPORTED = -2,/* valid but not compiled in (e.g. head_dim 200) */
+  IKL_ELAUNCH = -3,     /* HIP launch / runtime error */
+  IKL_EWORKSPACE = -4,  /* workspace missing or too small */
+};
+
+/* Kernel family chosen for a grouped-attention launch
+ * (ikl_paged_attention_path). */
+enum ikl_attention_path {
+  IKL_PATH_MHA_FALLBACK = 0,  /* heads_per_kv == 1: one query head per K/V tile */
+  IKL_PATH_SCALAR_GROUPED = 1,/* VALU path: query group shares each K/V tile */
+  IKL_PATH_MFMA_GROUPED = 2,  /* MFMA QK^T/PV tiles (dense group x tile) */
+};
+
+/* Arguments of ikl_append_kv.
+ * Replaces the launch in append.py:69-106 (append_kv_triton ->
+ * _append_kv_kernel, append.py:19-66) and the torch index_put of
+ * cache.py:156-189 (PagedKVCache.write_slots). */
+typedef struct ikl_append_args {
+  const void *key;           /* [num_tokens, num_kv_heads, head_dim] */
+  const void *value;         /* same shape as key */
+  int64_t key_stride_t, key_stride_h;
+  int64_t value_stride_t, value_stride_h;
+  const void *slots;         /* [num_tokens] physical slot = block*block_size + offset */
+  int32_t slot_type;         /* enum ikl_index_type */
+  void *k_cache;             /* base of cache.k[layer]: [num_blocks, block_size, kv_heads, head_dim] */
+  void *v_cache;             /* base of cache.v[layer] */
+  int64_t k_stride_block, k_stride_token, k_stride_head;
+  int64_t v_stride_block, v_stride_token, v_stride_head;
+  int64_t num_tokens;
+  int64_t num_blocks;
+  int32_t block_size;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t dtype;             /* enum ikl_dtype (key, value and cache share it) */
+} ikl_append_args;
+
+/* Arguments of ikl_paged_attention.
+ * Replaces paged_decode_attention_triton (triton_ops.py:404-478, kernel
+ * triton_ops.py:88-167) and paged_decode_attention_triton_grouped
+ * (triton_ops.py:481-610, kernels triton_ops.py:178-283 and 294-401). */
+typedef struct ikl_paged_attention_args {
+  const void *query;         /* [batch, num_heads, head_dim] */
+  int64_t q_stride_b, q_stride_h;
+  const void *k_cache;       /* base of cache.k[layer] */
+  const void *v_cache;       /* base of cache.v[layer] */
+  int64_t k_stride_block, k_stride_token, k_stride_head;
+  int64_t v_stride_block, v_stride_token, v_stride_head;
+  const void *block_tables;  /* [batch, table_width] physical block ids */
+  int32_t table_type;        /* enum ikl_index_type */
+  int64_t table_stride_b;
+  int64_t table_width;
+  const void *context_lens;  /* [batch] */
+  int32_t lens_type;         /* enum ikl_index_type */
+  void *out;                 /* [batch, num_heads, head_dim], dtype of query */
+  int64_t out_stride_b, out_stride_h;
+  int64_t batch;
+  int64_t num_blocks;
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t block_size;
+  int32_t dtype;             /* enum ikl_dtype (query, cache and out share it) */
+  float scale;               /* softmax scale; the reference default is head_dim**-0.5 */
+  /* Query heads that share one K/V tile inside a workgroup: 0 = all heads
+   * of a KV head (capped by the kernel family), else 1..heads_per_kv. */
+  int32_t query_group_size;
+  /* Tokens per split-context partition: 0 = pick automatically, -1 = never
+   * split (one pass per request), else a positive multiple of 64. */
+  int32_t partition_size;
+  /* Host-known upper bound of context_lens (0 = table_width*block_size);
+   * only sizes the grid, never read from device memory. */
+  int64_t max_context_len;
+  /* Kernel family: -1 = automatic (ikl_paged_attention_path), else an
+   * enum ikl_attention_path value. */
+  int32_t path;
+  /* Scratch for split partials; size from ikl_paged_attention_workspace_size. */
+  void *workspace;
+  int64_t workspace_bytes;
+  /* Optional hipEvent_t handles recorded on `stream` for timing single
+   * kernels of the launch: [0] before the attention kernel, [1] after it,
+   * [2] after the split reduce kernel. NULL entries are skipped. */
+  void *events[3];
+} ikl_paged_attention_args;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *ikl_last_error(void);
+
+/* Library version string. */
+const char *ikl_version(void);
+
+/* KV append (in place). Slots outside [0, num_blocks*block_size) are skipped,
+ * never written. Replaces append.py:69-106 / cache.py:156-189. */
+int ikl_append_kv(const ikl_append_args *args, void *stream);
+
+/* Bytes of workspace the launch described by `args` needs (0 when it runs
+ * without split partials). Negative on invalid arguments. */
+int64_t ikl_paged_attention_workspace_size(const ikl_paged_attention_args *args);
+
+/* Resolved split partition size (tokens) for `args`, or 0 when the launch
+ * runs without splitting. Negative on invalid arguments. */
+int32_t ikl_paged_attention_partition_size(const ikl_paged_attention_args *args);
+
+/* Paged decode attention. Positions p < context_lens[b] whose physical block
+ * id is outside [0, num_blocks) are masked (like triton_ops.py:138); the
+ * kernels never read outside the cache. Replaces triton_ops.py:404-610. */
+int ikl_paged_attention(const ikl_paged_attention_args *args, void *stream);
+
+/* Static path selection for a grouped launch; mirrors the role of
+ * paged_decode_grouped_path (triton_ops.py:56-75) for this library's
+ * kernel families. dtype: enum ikl_dtype. Returns enum ikl_attention_path. */
+int32_t ikl_paged_attention_path(int32_t dtype, int32_t head_dim, int64_t table_width,
+                                 int32_t heads_per_kv, int32_t query_group_size);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IKL_PAGED_H */

@@ -1,0 +1,45 @@
+"""MI355X (gfx950) paged-KV decode path for InferKernelLab.
+
+Hand-written HIP kernels (KV append, paged decode attention with split
+partitions) behind the C ABI of include/ikl_paged.h, with the reference's
+operator surface (ops), paged cache (cache), scheduler and runtime hooks.
+"""
+
+from .cache import BlockAllocator, CacheLayout, PagedKVCache
+from .ops import (
+    append_kv_hip,
+    append_kv_triton,
+    hip_append_available,
+    hip_available,
+    paged_decode_attention_hip,
+    paged_decode_attention_hip_grouped,
+    paged_decode_attention_triton,
+    paged_decode_attention_triton_grouped,
+    paged_decode_grouped_path,
+    triton_append_available,
+    triton_available,
+)
+from .runtime import InferenceRuntime, RuntimeStats
+from .scheduler import InferenceRequest, ScheduleBatch, TokenBudgetScheduler
+
+__all__ = [
+    "BlockAllocator",
+    "CacheLayout",
+    "PagedKVCache",
+    "InferenceRequest",
+    "ScheduleBatch",
+    "TokenBudgetScheduler",
+    "InferenceRuntime",
+    "RuntimeStats",
+    "append_kv_hip",
+    "append_kv_triton",
+    "hip_available",
+    "hip_append_available",
+    "paged_decode_attention_hip",
+    "paged_decode_attention_hip_grouped",
+    "paged_decode_attention_triton",
+    "paged_decode_attention_triton_grouped",
+    "paged_decode_grouped_path",
+    "triton_available",
+    "triton_append_available",
+]

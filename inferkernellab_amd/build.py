@@ -1,0 +1,79 @@
+"""Builds libikl_paged.so (the gfx950 HIP kernels behind the C ABI of
+include/ikl_paged.h) in-tree with hipcc.
+
+Usage: ``python -m inferkernellab_amd.build`` (or ``build()`` from Python).
+Each ``.hip`` file is compiled to an object in parallel, then linked into
+``inferkernellab_amd/libikl_paged.so`` with an atomic rename.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+CSRC = PACKAGE_DIR / "csrc"
+BUILD_DIR = PACKAGE_DIR / "_build"
+LIB_NAME = "libikl_paged.so"
+LIB_PATH = PACKAGE_DIR / LIB_NAME
+ARCH = "gfx950"
+
+SOURCES = ("abi.hip", "append_kv.hip", "paged_decode.hip")
+
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    # Packed fp32 VALU ops are kept out of the device code on purpose.
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def _hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(path).exists():
+        raise RuntimeError("hipcc not found; ROCm is required to build libikl_paged.so")
+    return path
+
+
+def _compile(hipcc: str, src: Path, obj: Path, extra: list[str]) -> None:
+    cmd = [hipcc, *COMMON_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{result.stdout}\n{result.stderr}")
+
+
+def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
+    """Compile every HIP source for gfx950 and link libikl_paged.so."""
+    hipcc = _hipcc()
+    extra = list(extra_flags or [])
+    BUILD_DIR.mkdir(exist_ok=True)
+    objs = [BUILD_DIR / (name.replace(".hip", ".o")) for name in SOURCES]
+    jobs = min(len(SOURCES), max(1, os.cpu_count() or 1))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        futures = [
+            pool.submit(_compile, hipcc, CSRC / name, obj, extra) for name, obj in zip(SOURCES, objs)
+        ]
+        for future in futures:
+            future.result()
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"link failed:\n{result.stdout}\n{result.stderr}")
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH}")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build(verbose=True)

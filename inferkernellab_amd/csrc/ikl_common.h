@@ -1,0 +1,127 @@
+// Shared device helpers for the gfx950 paged-decode kernels: element
+// traits for fp16 / bf16 / fp32, 16-byte vector loads, dot products on
+// packed halves, wave-level DPP reductions and the thread-local error slot
+// of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/ikl_paged.h"
+
+namespace ikl {
+
+// ---------------------------------------------------------------- errors
+void set_error(const std::string &msg);
+int fail(int code, const std::string &msg);
+int check_launch(const char *what);
+
+// ---------------------------------------------------------- element types
+struct f16_tag {};
+struct bf16_tag {};
+struct f32_tag {};
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf162_t __attribute__((ext_vector_type(2)));
+
+template <typename Tag> struct elem;
+
+template <> struct elem<f16_tag> {
+  static constexpr int bytes = 2;
+  static constexpr int vec = 8;  // elements per 16-byte chunk
+  __device__ static inline float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(half2_t, w)[0];
+  }
+  __device__ static inline float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(half2_t, w)[1];
+  }
+  // fp32 accumulate of a.lo*b.lo + a.hi*b.hi + c.
+  __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b),
+                                  c, false);
+  }
+  __device__ static inline uint32_t pack2(float a, float b) {
+    half2_t h = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, h);
+  }
+};
+
+__device__ inline uint32_t f32_to_bf16_bits(float f) {
+  // Round to nearest even, NaN kept quiet (matches torch's float->bfloat16).
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+template <> struct elem<bf16_tag> {
+  static constexpr int bytes = 2;
+  static constexpr int vec = 8;
+  __device__ static inline float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  __device__ static inline float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf162_t, a),
+                                           __builtin_bit_cast(bf162_t, b), c, false);
+  }
+  __device__ static inline uint32_t pack2(float a, float b) {
+    return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+  }
+};
+
+template <> struct elem<f32_tag> {
+  static constexpr int bytes = 4;
+  static constexpr int vec = 4;
+};
+
+// ------------------------------------------------------------ wave helpers
+// DPP controls (gfx9 encoding).
+constexpr int DPP_QUAD_XOR1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;  // lane i <-> 7-i within 8
+constexpr int DPP_ROW_MIRROR = 0x140;       // lane i <-> 15-i within 16
+
+template <int CTRL>
+__device__ inline float dpp_mov(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of N contiguous lanes (N in 1,2,4,8,16); every lane
+// of the group receives the group sum. Uses pairings (xor1, xor2, half
+// mirror, mirror) whose composition covers each group exactly once.
+template <int N>
+__device__ inline float group_sum(float v) {
+  if constexpr (N >= 2) v += dpp_mov<DPP_QUAD_XOR1>(v);
+  if constexpr (N >= 4) v += dpp_mov<DPP_QUAD_XOR2>(v);
+  if constexpr (N >= 8) v += dpp_mov<DPP_ROW_HALF_MIRROR>(v);
+  if constexpr (N >= 16) v += dpp_mov<DPP_ROW_MIRROR>(v);
+  static_assert(N <= 16, "group_sum supports up to 16 lanes");
+  return v;
+}
+
+__device__ inline float shfl_xor_f(float v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+
+struct alignas(16) u32x4 {
+  uint32_t x, y, z, w;
+};
+
+__device__ inline u32x4 load16(const void *p) {
+  return *reinterpret_cast<const u32x4 *>(p);
+}
+__device__ inline void store16(void *p, const u32x4 &v) {
+  *reinterpret_cast<u32x4 *>(p) = v;
+}
+__device__ inline uint32_t u32x4_at(const u32x4 &v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+template <typename IdxT>
+__device__ inline int64_t load_index(const void *base, int64_t i) {
+  return (int64_t)(reinterpret_cast<const IdxT *>(base)[i]);
+}
+
+}  // namespace ikl

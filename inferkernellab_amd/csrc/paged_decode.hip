@@ -1,0 +1,662 @@
+// Paged decode attention for gfx950: VALU ("scalar") kernel family, the
+// split-context reduce kernel and the ikl_paged_attention entry point.
+//
+// Computes, per request b and query head h (kv head = h / (H/Hkv), the map
+// of attention.py:9-15 and triton_ops.py:123):
+//   out[b,h,:] = softmax(scale * q[b,h,:] . K[b,:ctx_b,kvh,:]) @ V[b,:ctx_b,kvh,:]
+// where token p of request b lives at cache[table[b, p / bs], p % bs]
+// (cache.py:113-129, 191-200), like paged_reference (attention.py:134-175).
+//
+// Launch geometry (one wave64 per workgroup):
+//   grid.x = split-context partition (1 when not split)
+//   grid.y = kv_head * groups_per_kv + query_group
+//   grid.z = request
+// Each workgroup streams the K/V rows of its partition ONCE and applies them
+// to all G query heads of its group (G = H/Hkv for GQA; the reference's
+// per-head kernel re-reads K/V G times, triton_ops.py:465).
+//
+// Lane layout: TPT lanes share one token; lane `sub` of the token owns the
+// 16-byte chunks c*TPT+sub (c < CPL) of the head_dim row, so the TPT lanes
+// of a token read TPT*16 contiguous bytes per load instruction. A wave
+// covers ROWS = 64/TPT tokens per row-step and R row-steps per tile.
+// QK^T: packed-half dot products (v_dot2_f32_{f16,bf16}) + DPP group sum.
+// Softmax: every token row keeps its own online (max, sum, acc) in the
+// log2 domain, rescaled lazily (only when the max grows by more than
+// RESCALE_LOG2); rows merge once at the end of the partition.
+// PV: fp32 FMAs on converted V.
+#include <math.h>
+
+#include <algorithm>
+#include <string>
+
+#include "ikl_common.h"
+
+namespace ikl {
+namespace {
+
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float NEG_SENTINEL = -1.0e30f;  // finite "minus infinity" for running maxima
+constexpr float RESCALE_LOG2 = 8.0f;      // lazy-rescale threshold (factor 256)
+
+struct AttnParams {
+  const char *q;
+  int64_t q_sb, q_sh;  // elements
+  const char *kc;
+  const char *vc;
+  int64_t k_sb, k_st, k_sh;  // elements
+  int64_t v_sb, v_st, v_sh;  // elements
+  const void *tables;
+  int64_t t_sb;
+  int64_t table_width;
+  const void *lens;
+  char *out;
+  int64_t o_sb, o_sh;  // elements
+  float *part_o;       // [B, H, NP, D] fp32 (split only)
+  float *part_lse;     // [B, H, NP] fp32, log2 domain (split only)
+  int64_t num_blocks;
+  int32_t num_heads;
+  int32_t heads_per_kv;
+  int32_t group_size;
+  int32_t groups_per_kv;
+  int32_t block_size;
+  int32_t bs_shift;        // log2(block_size) or -1
+  int32_t partition_size;  // tokens per grid.x slot
+  int32_t num_parts;       // NP (grid.x)
+  int32_t split;           // write partials instead of the output
+  int32_t table_i64;
+  int32_t lens_i64;
+  float scale_log2;        // scale * log2(e)
+};
+
+constexpr int pow2_divisor(int n, int cap) {
+  int t = 1;
+  while (t * 2 <= cap && n % (t * 2) == 0) t *= 2;
+  return t;
+}
+
+template <typename Tag, int D, int G>
+struct ScalarCfg {
+  static constexpr int EB = elem<Tag>::bytes;
+  static constexpr int VEC = 16 / EB;              // elements per 16-byte chunk
+  static constexpr int NCHUNK = D / VEC;           // chunks per head_dim row
+  static_assert(D % VEC == 0, "head_dim must be a multiple of a 16-byte chunk");
+  static constexpr int TPT = pow2_divisor(NCHUNK, G >= 8 ? 16 : 8);  // lanes per token
+  static constexpr int CPL = NCHUNK / TPT;         // chunks per lane
+  static constexpr int LD = CPL * VEC;             // dims per lane
+  static constexpr int ROWS = 64 / TPT;            // tokens per row-step
+  static constexpr int R = CPL >= 4 ? 1 : 4 / CPL; // row-steps per tile
+  static constexpr int TI = ROWS * R;              // tokens per tile
+};
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <typename Tag>
+__device__ inline void store_out_chunk(char *dst, const float *v);
+
+template <>
+__device__ inline void store_out_chunk<bf16_tag>(char *dst, const float *v) {
+  u32x4 w;
+  w.x = elem<bf16_tag>::pack2(v[0], v[1]);
+  w.y = elem<bf16_tag>::pack2(v[2], v[3]);
+  w.z = elem<bf16_tag>::pack2(v[4], v[5]);
+  w.w = elem<bf16_tag>::pack2(v[6], v[7]);
+  store16(dst, w);
+}
+template <>
+__device__ inline void store_out_chunk<f16_tag>(char *dst, const float *v) {
+  u32x4 w;
+  w.x = elem<f16_tag>::pack2(v[0], v[1]);
+  w.y = elem<f16_tag>::pack2(v[2], v[3]);
+  w.z = elem<f16_tag>::pack2(v[4], v[5]);
+  w.w = elem<f16_tag>::pack2(v[6], v[7]);
+  store16(dst, w);
+}
+template <>
+__device__ inline void store_out_chunk<f32_tag>(char *dst, const float *v) {
+  u32x4 w;
+  w.x = __float_as_uint(v[0]);
+  w.y = __float_as_uint(v[1]);
+  w.z = __float_as_uint(v[2]);
+  w.w = __float_as_uint(v[3]);
+  store16(dst, w);
+}
+
+// Loads the window of 64 block-table entries starting at logical block
+// `base`; entries outside the table or naming a block outside the cache
+// become -1 (masked).
+__device__ inline int load_table_window(const AttnParams &p, int64_t b, int64_t base, int lane) {
+  const int64_t lb = base + lane;
+  int phys = -1;
+  if (lb < p.table_width) {
+    const int64_t e = p.table_i64 ? load_index<int64_t>(p.tables, b * p.t_sb + lb)
+                                  : load_index<int32_t>(p.tables, b * p.t_sb + lb);
+    if (e >= 0 && e < p.num_blocks) phys = (int)e;
+  }
+  return phys;
+}
+
+template <typename Tag, int D, int G>
+__global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParams p) {
+  using C = ScalarCfg<Tag, D, G>;
+  constexpr int TPT = C::TPT, CPL = C::CPL, LD = C::LD, ROWS = C::ROWS, R = C::R, TI = C::TI;
+  constexpr int VEC = C::VEC, EB = C::EB;
+  constexpr bool F32 = (EB == 4);
+  constexpr int QW = F32 ? 4 : 4;  // 32-bit words per chunk
+
+  const int lane = threadIdx.x;
+  const int row = lane / TPT;
+  const int sub = lane % TPT;
+  const int part = blockIdx.x;
+  const int kvh = blockIdx.y / p.groups_per_kv;
+  const int qg = blockIdx.y % p.groups_per_kv;
+  const int64_t b = blockIdx.z;
+
+  const int64_t ctx = p.lens_i64 ? load_index<int64_t>(p.lens, b) : load_index<int32_t>(p.lens, b);
+  const int64_t part_start = (int64_t)part * p.partition_size;
+  if (part > 0 && part_start >= ctx) return;  // no tokens for this partition
+  const int64_t part_end = ctx < part_start + p.partition_size ? ctx : part_start + p.partition_size;
+  const int n_tiles = part_end > part_start ? (int)((part_end - part_start + TI - 1) / TI) : 0;
+
+  // ---- query heads of this group
+  const int head0 = qg * p.group_size;  // index inside the kv head's heads
+  uint32_t qw[G][CPL][QW];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const bool hv = (g < p.group_size) && (head0 + g < p.heads_per_kv);
+    const int64_t hq = (int64_t)kvh * p.heads_per_kv + head0 + g;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (hv) v = load16(p.q + (b * p.q_sb + hq * p.q_sh + (int64_t)(c * TPT + sub) * VEC) * EB);
+      qw[g][c][0] = v.x;
+      qw[g][c][1] = v.y;
+      qw[g][c][2] = v.z;
+      qw[g][c][3] = v.w;
+    }
+  }
+
+  float m[G], l[G], acc[G][LD];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = NEG_SENTINEL;
+    l[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < LD; ++i) acc[g][i] = 0.f;
+  }
+
+  const char *kbase = p.kc + (int64_t)kvh * p.k_sh * EB;
+  const char *vbase = p.vc + (int64_t)kvh * p.v_sh * EB;
+  const int bs = p.block_size;
+
+  // Block-table window: lane j holds table[b, win_base + j].
+  int64_t win_base = -1000000;
+  int win = -1;
+
+  // Resolves the physical block of every row-step token of tile `t` and
+  // issues its K/V loads.
+  auto load_tile = [&](int t, u32x4 (&kr)[R][CPL], u32x4 (&vr)[R][CPL], uint32_t &valid) {
+    const int64_t tile_base = part_start + (int64_t)t * TI;
+    const int64_t lb_lo = p.bs_shift >= 0 ? (tile_base >> p.bs_shift) : tile_base / bs;
+    const int64_t last = tile_base + TI - 1;
+    const int64_t lb_hi = p.bs_shift >= 0 ? (last >> p.bs_shift) : last / bs;
+    if (lb_lo < win_base || lb_hi >= win_base + 64) {
+      win_base = lb_lo;
+      win = load_table_window(p, b, win_base, lane);
+    }
+    valid = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t pos = tile_base + r * ROWS + row;
+      const int64_t lb = p.bs_shift >= 0 ? (pos >> p.bs_shift) : pos / bs;
+      const int64_t off = pos - lb * bs;
+      const int64_t idx = lb - win_base;
+      int phys = __builtin_amdgcn_ds_bpermute((int)(idx & 63) * 4, win);
+      if (idx >= 64) phys = load_table_window(p, b, lb, 0);  // tile wider than the window
+      const bool ok = (pos < part_end) && (phys >= 0);
+      valid |= (ok ? 1u : 0u) << r;
+      if (ok) {
+        const char *kr_row = kbase + ((int64_t)phys * p.k_sb + off * p.k_st) * EB;
+        const char *vr_row = vbase + ((int64_t)phys * p.v_sb + off * p.v_st) * EB;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          kr[r][c] = load16(kr_row + (c * TPT + sub) * 16);
+          vr[r][c] = load16(vr_row + (c * TPT + sub) * 16);
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          kr[r][c] = u32x4{0u, 0u, 0u, 0u};
+          vr[r][c] = u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+    }
+  };
+
+  auto compute_tile = [&](const u32x4 (&kr)[R][CPL], const u32x4 (&vr)[R][CPL], uint32_t valid) {
+    float s[R][G];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const uint32_t kw = u32x4_at(kr[r][c], w);
+            if constexpr (F32) {
+              d = fmaf(__uint_as_float(kw), __uint_as_float(qw[g][c][w]), d);
+            } else {
+              d = elem<Tag>::dot2(kw, qw[g][c][w], d);
+            }
+          }
+        }
+        d = group_sum<TPT>(d) * p.scale_log2;
+        s[r][g] = ((valid >> r) & 1u) ? d : -INFINITY;
+      }
+    }
+    // Lazy online-softmax rescale.
+    bool need_any = false;
+    float tmax[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float t = s[0][g];
+#pragma unroll
+      for (int r = 1; r < R; ++r) t = fmaxf(t, s[r][g]);
+      tmax[g] = t;
+      need_any |= t > m[g] + RESCALE_LOG2;
+    }
+    if (__builtin_amdgcn_ballot_w64(need_any) != 0ull) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const bool need = tmax[g] > m[g] + RESCALE_LOG2;
+        const float alpha = need ? fast_exp2(m[g] - tmax[g]) : 1.f;
+        m[g] = need ? tmax[g] : m[g];
+        l[g] *= alpha;
+#pragma unroll
+        for (int i = 0; i < LD; ++i) acc[g][i] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float pr[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        pr[g] = fast_exp2(s[r][g] - m[g]);
+        l[g] += pr[g];
+      }
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t vw = u32x4_at(vr[r][c], w);
+          if constexpr (F32) {
+            const float v0 = __uint_as_float(vw);
+#pragma unroll
+            for (int g = 0; g < G; ++g) acc[g][c * VEC + w] = fmaf(pr[g], v0, acc[g][c * VEC + w]);
+          } else {
+            const float v0 = elem<Tag>::lo(vw);
+            const float v1 = elem<Tag>::hi(vw);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              acc[g][c * VEC + 2 * w] = fmaf(pr[g], v0, acc[g][c * VEC + 2 * w]);
+              acc[g][c * VEC + 2 * w + 1] = fmaf(pr[g], v1, acc[g][c * VEC + 2 * w + 1]);
+            }
+          }
+        }
+      }
+    }
+  };
+
+  // ---- software-pipelined tile loop: loads of tile t+1 fly while tile t computes
+  u32x4 ka[R][CPL], va[R][CPL], kb[R][CPL], vb[R][CPL];
+  uint32_t valid_a = 0, valid_b = 0;
+  if (n_tiles > 0) load_tile(0, ka, va, valid_a);
+  int t = 0;
+  for (; t + 1 < n_tiles; t += 2) {
+    load_tile(t + 1, kb, vb, valid_b);
+    compute_tile(ka, va, valid_a);
+    if (t + 2 < n_tiles) load_tile(t + 2, ka, va, valid_a);
+    compute_tile(kb, vb, valid_b);
+  }
+  if (t < n_tiles) compute_tile(ka, va, valid_a);
+
+  // ---- merge the token rows of the wave (same sub, different row)
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mx = m[g];
+#pragma unroll
+    for (int mask = TPT; mask < 64; mask <<= 1) mx = fmaxf(mx, shfl_xor_f(mx, mask));
+    const float w = fast_exp2(m[g] - mx);
+    l[g] *= w;
+#pragma unroll
+    for (int mask = TPT; mask < 64; mask <<= 1) l[g] += shfl_xor_f(l[g], mask);
+#pragma unroll
+    for (int i = 0; i < LD; ++i) {
+      float a = acc[g][i] * w;
+#pragma unroll
+      for (int mask = TPT; mask < 64; mask <<= 1) a += shfl_xor_f(a, mask);
+      acc[g][i] = a;
+    }
+    m[g] = mx;
+  }
+
+  // ---- write: row r writes the heads g with g % ROWS == r
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if ((g % ROWS) != row) continue;
+    if (!(g < p.group_size && head0 + g < p.heads_per_kv)) continue;
+    const int64_t hq = (int64_t)kvh * p.heads_per_kv + head0 + g;
+    if (p.split) {
+      const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;
+      const int64_t prow = (b * p.num_heads + hq) * p.num_parts + part;
+      float *po = p.part_o + prow * D;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+#pragma unroll
+        for (int e = 0; e < VEC; e += 4) {
+          u32x4 w;
+          w.x = __float_as_uint(acc[g][c * VEC + e] * inv);
+          w.y = __float_as_uint(acc[g][c * VEC + e + 1] * inv);
+          w.z = __float_as_uint(acc[g][c * VEC + e + 2] * inv);
+          w.w = __float_as_uint(acc[g][c * VEC + e + 3] * inv);
+          store16(po + (c * TPT + sub) * VEC + e, w);
+        }
+      }
+      if (sub == 0) p.part_lse[prow] = l[g] > 0.f ? m[g] + log2f(l[g]) : -INFINITY;
+    } else {
+      const float inv = 1.f / l[g];  // l == 0 (no valid token) gives NaN, like the reference
+      char *dst = p.out + (b * p.o_sb + hq * p.o_sh) * EB;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        float v[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[e] = acc[g][c * VEC + e] * inv;
+        store_out_chunk<Tag>(dst + (int64_t)(c * TPT + sub) * 16, v);
+      }
+    }
+  }
+}
+
+// Combines the split partials of one (request, head):
+//   out = sum_p 2^(lse_p - M) o_p / sum_p 2^(lse_p - M),  M = max_p lse_p.
+template <typename Tag, int D>
+__global__ __launch_bounds__(64) void paged_decode_reduce_kernel(const AttnParams p) {
+  constexpr int EB = elem<Tag>::bytes;
+  const int lane = threadIdx.x;
+  const int64_t hq = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int64_t ctx = p.lens_i64 ? load_index<int64_t>(p.lens, b) : load_index<int32_t>(p.lens, b);
+  int np = ctx > 0 ? (int)((ctx + p.partition_size - 1) / p.partition_size) : 0;
+  if (np > p.num_parts) np = p.num_parts;
+  const int64_t prow = (b * p.num_heads + hq) * p.num_parts;
+  float mx = -INFINITY;
+  for (int i = lane; i < np; i += 64) mx = fmaxf(mx, p.part_lse[prow + i]);
+#pragma unroll
+  for (int mask = 1; mask < 64; mask <<= 1) mx = fmaxf(mx, shfl_xor_f(mx, mask));
+  constexpr int PER = (D + 63) / 64;
+  float accv[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) accv[j] = 0.f;
+  float z = 0.f;
+  for (int i = 0; i < np; ++i) {
+    const float w = fast_exp2(p.part_lse[prow + i] - mx);
+    z += w;
+    const float *po = p.part_o + (prow + i) * D;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int d = lane + 64 * j;
+      if (d < D) accv[j] = fmaf(w, po[d], accv[j]);
+    }
+  }
+  const float inv = 1.f / z;
+  char *dst = p.out + (b * p.o_sb + hq * p.o_sh) * EB;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int d = lane + 64 * j;
+    if (d >= D) continue;
+    const float v = accv[j] * inv;
+    if constexpr (EB == 4) {
+      reinterpret_cast<float *>(dst)[d] = v;
+    } else if constexpr (__is_same(Tag, bf16_tag)) {
+      reinterpret_cast<uint16_t *>(dst)[d] = (uint16_t)f32_to_bf16_bits(v);
+    } else {
+      reinterpret_cast<_Float16 *>(dst)[d] = (_Float16)v;
+    }
+  }
+}
+
+// ------------------------------------------------------------ host side
+
+struct Plan {
+  int eb = 0;
+  int path = IKL_PATH_SCALAR_GROUPED;
+  int heads_per_kv = 0;
+  int group_size = 0;
+  int gmax = 0;
+  int groups_per_kv = 0;
+  int partition = 0;  // tokens per grid.x slot
+  int num_parts = 1;
+  bool split = false;
+  int64_t ws_o_bytes = 0;
+  int64_t ws_bytes = 0;
+};
+
+int elem_bytes(int dtype) {
+  switch (dtype) {
+    case IKL_F16:
+    case IKL_BF16: return 2;
+    case IKL_F32: return 4;
+    default: return 0;
+  }
+}
+
+bool head_dim_supported(int d) { return d == 16 || d == 32 || d == 64 || d == 96 || d == 128; }
+
+int next_pow2(int x) {
+  int v = 1;
+  while (v < x) v *= 2;
+  return v;
+}
+
+constexpr int SCALAR_MAX_GROUP = 8;
+
+int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
+  if (!a) return fail(IKL_EINVAL, "attention: null argument struct");
+  pl.eb = elem_bytes(a->dtype);
+  if (!pl.eb) return fail(IKL_EINVAL, "attention: unsupported dtype");
+  if (a->batch <= 0 || a->num_heads <= 0 || a->num_kv_heads <= 0 || a->head_dim <= 0)
+    return fail(IKL_EINVAL, "query dimensions must be positive");
+  if (a->num_heads % a->num_kv_heads != 0)
+    return fail(IKL_EINVAL, "num_heads must be divisible by num_kv_heads");
+  if (a->block_size <= 0 || a->num_blocks <= 0)
+    return fail(IKL_EINVAL, "cache dimensions must be positive");
+  if (a->num_blocks > 0x7fffffffLL) return fail(IKL_EINVAL, "num_blocks must fit in int32");
+  if (a->table_width <= 0) return fail(IKL_EINVAL, "block_tables must contain at least one logical block");
+  if (a->table_type != IKL_I32 && a->table_type != IKL_I64)
+    return fail(IKL_EINVAL, "block_tables must use int32 or int64");
+  if (a->lens_type != IKL_I32 && a->lens_type != IKL_I64)
+    return fail(IKL_EINVAL, "context_lens must use int32 or int64");
+  if (!head_dim_supported(a->head_dim))
+    return fail(IKL_EUNSUPPORTED, "head_dim " + std::to_string(a->head_dim) +
+                                      " is not compiled (supported: 16, 32, 64, 96, 128)");
+  if (a->batch > 65535) return fail(IKL_EINVAL, "batch exceeds the grid limit (65535)");
+  pl.heads_per_kv = a->num_heads / a->num_kv_heads;
+  pl.path = IKL_PATH_SCALAR_GROUPED;
+  if (a->path == IKL_PATH_MHA_FALLBACK || pl.heads_per_kv == 1) pl.path = IKL_PATH_MHA_FALLBACK;
+  int gs = a->query_group_size;
+  if (gs < 0) return fail(IKL_EINVAL, "query_group_size must be non-negative");
+  if (gs == 0 || gs > pl.heads_per_kv) gs = pl.heads_per_kv;
+  if (pl.path == IKL_PATH_MHA_FALLBACK) gs = 1;
+  if (gs > SCALAR_MAX_GROUP) gs = SCALAR_MAX_GROUP;
+  pl.group_size = gs;
+  pl.gmax = next_pow2(gs);
+  pl.groups_per_kv = (pl.heads_per_kv + gs - 1) / gs;
+
+  // Split-context partitions.
+  const int64_t cap = a->table_width * (int64_t)a->block_size;
+  int64_t maxctx = a->max_context_len > 0 ? std::min<int64_t>(a->max_context_len, cap) : cap;
+  const int64_t units = a->batch * (int64_t)a->num_kv_heads * pl.groups_per_kv;
+  int64_t P;
+  if (a->partition_size == -1) {
+    P = maxctx;
+  } else if (a->partition_size > 0) {
+    if (a->partition_size % 64 != 0)
+      return fail(IKL_EINVAL, "partition_size must be a positive multiple of 64");
+    P = a->partition_size;
+  } else {
+    P = 512;
+    const int64_t target = 2048;  // workgroups that keep 256 CUs busy
+    while (P > 128 && units * ((maxctx + P - 1) / P) < target) P /= 2;
+  }
+  if (P >= maxctx) {
+    pl.split = false;
+    pl.num_parts = 1;
+    pl.partition = (int)std::min<int64_t>(std::max<int64_t>(cap, maxctx), 0x7fffffffLL);
+  } else {
+    pl.split = true;
+    const int64_t np = (maxctx + P - 1) / P;
+    if (np > 65535) return fail(IKL_EINVAL, "too many split partitions for one launch");
+    pl.num_parts = (int)np;
+    pl.partition = (int)P;
+  }
+  if (pl.split) {
+    const int64_t rows = a->batch * (int64_t)a->num_heads * pl.num_parts;
+    pl.ws_o_bytes = ((rows * a->head_dim * 4) + 255) / 256 * 256;
+    pl.ws_bytes = pl.ws_o_bytes + rows * 4;
+  }
+  return IKL_OK;
+}
+
+void record(void *ev, hipStream_t s) {
+  if (ev) (void)hipEventRecord((hipEvent_t)ev, s);
+}
+
+template <typename Tag, int D>
+hipError_t launch_scalar(const Plan &pl, const AttnParams &p, dim3 grid, hipStream_t s,
+                         void *const *events) {
+  record(events[0], s);
+  switch (pl.gmax) {
+    case 1: paged_decode_scalar_kernel<Tag, D, 1><<<grid, 64, 0, s>>>(p); break;
+    case 2: paged_decode_scalar_kernel<Tag, D, 2><<<grid, 64, 0, s>>>(p); break;
+    case 4: paged_decode_scalar_kernel<Tag, D, 4><<<grid, 64, 0, s>>>(p); break;
+    default: paged_decode_scalar_kernel<Tag, D, 8><<<grid, 64, 0, s>>>(p); break;
+  }
+  record(events[1], s);
+  if (pl.split) {
+    dim3 rgrid((unsigned)p.num_heads, grid.z);
+    paged_decode_reduce_kernel<Tag, D><<<rgrid, 64, 0, s>>>(p);
+  }
+  record(events[2], s);
+  return hipGetLastError();
+}
+
+template <typename Tag>
+hipError_t launch_dim(int d, const Plan &pl, const AttnParams &p, dim3 grid, hipStream_t s,
+                      void *const *ev) {
+  switch (d) {
+    case 16: return launch_scalar<Tag, 16>(pl, p, grid, s, ev);
+    case 32: return launch_scalar<Tag, 32>(pl, p, grid, s, ev);
+    case 64: return launch_scalar<Tag, 64>(pl, p, grid, s, ev);
+    case 96: return launch_scalar<Tag, 96>(pl, p, grid, s, ev);
+    default: return launch_scalar<Tag, 128>(pl, p, grid, s, ev);
+  }
+}
+
+bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+}  // namespace
+}  // namespace ikl
+
+using namespace ikl;
+
+extern "C" int64_t ikl_paged_attention_workspace_size(const ikl_paged_attention_args *a) {
+  Plan pl;
+  int rc = make_plan(a, pl);
+  if (rc != IKL_OK) return rc;
+  return pl.ws_bytes;
+}
+
+extern "C" int32_t ikl_paged_attention_partition_size(const ikl_paged_attention_args *a) {
+  Plan pl;
+  int rc = make_plan(a, pl);
+  if (rc != IKL_OK) return rc;
+  return pl.split ? pl.partition : 0;
+}
+
+extern "C" int32_t ikl_paged_attention_path(int32_t dtype, int32_t head_dim, int64_t table_width,
+                                            int32_t heads_per_kv, int32_t query_group_size) {
+  (void)dtype;
+  (void)head_dim;
+  (void)table_width;
+  (void)query_group_size;
+  if (heads_per_kv == 1) return IKL_PATH_MHA_FALLBACK;
+  return IKL_PATH_SCALAR_GROUPED;
+}
+
+extern "C" int ikl_paged_attention(const ikl_paged_attention_args *a, void *stream) {
+  Plan pl;
+  int rc = make_plan(a, pl);
+  if (rc != IKL_OK) return rc;
+  if (!a->query || !a->k_cache || !a->v_cache || !a->block_tables || !a->context_lens || !a->out)
+    return fail(IKL_EINVAL, "attention: null tensor pointer");
+  const int vec = 16 / pl.eb;
+  // 16-byte vector access needs every row start 16-byte aligned.
+  if (!aligned16(a->query) || !aligned16(a->k_cache) || !aligned16(a->v_cache) || !aligned16(a->out) ||
+      a->q_stride_b % vec || a->q_stride_h % vec || a->k_stride_block % vec ||
+      a->k_stride_token % vec || a->k_stride_head % vec || a->v_stride_block % vec ||
+      a->v_stride_token % vec || a->v_stride_head % vec || a->out_stride_b % vec ||
+      a->out_stride_h % vec)
+    return fail(IKL_EINVAL, "attention: query/cache/out rows must be 16-byte aligned");
+  if (pl.split && (!a->workspace || a->workspace_bytes < pl.ws_bytes || !aligned16(a->workspace)))
+    return fail(IKL_EWORKSPACE, "attention: workspace missing or smaller than " +
+                                    std::to_string(pl.ws_bytes) + " bytes");
+
+  AttnParams p;
+  p.q = (const char *)a->query;
+  p.q_sb = a->q_stride_b;
+  p.q_sh = a->q_stride_h;
+  p.kc = (const char *)a->k_cache;
+  p.vc = (const char *)a->v_cache;
+  p.k_sb = a->k_stride_block;
+  p.k_st = a->k_stride_token;
+  p.k_sh = a->k_stride_head;
+  p.v_sb = a->v_stride_block;
+  p.v_st = a->v_stride_token;
+  p.v_sh = a->v_stride_head;
+  p.tables = a->block_tables;
+  p.t_sb = a->table_stride_b;
+  p.table_width = a->table_width;
+  p.lens = a->context_lens;
+  p.out = (char *)a->out;
+  p.o_sb = a->out_stride_b;
+  p.o_sh = a->out_stride_h;
+  p.part_o = pl.split ? (float *)a->workspace : nullptr;
+  p.part_lse = pl.split ? (float *)((char *)a->workspace + pl.ws_o_bytes) : nullptr;
+  p.num_blocks = a->num_blocks;
+  p.num_heads = a->num_heads;
+  p.heads_per_kv = pl.heads_per_kv;
+  p.group_size = pl.group_size;
+  p.groups_per_kv = pl.groups_per_kv;
+  p.block_size = a->block_size;
+  p.bs_shift = -1;
+  for (int sh = 0; sh < 31; ++sh)
+    if ((1 << sh) == a->block_size) p.bs_shift = sh;
+  p.partition_size = pl.partition;
+  p.num_parts = pl.num_parts;
+  p.split = pl.split ? 1 : 0;
+  p.table_i64 = a->table_type == IKL_I64;
+  p.lens_i64 = a->lens_type == IKL_I64;
+  p.scale_log2 = a->scale * LOG2E;
+
+  dim3 grid((unsigned)pl.num_parts, (unsigned)(a->num_kv_heads * pl.groups_per_kv), (unsigned)a->batch);
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  switch (a->dtype) {
+    case IKL_F16: e = launch_dim<f16_tag>(a->head_dim, pl, p, grid, s, a->events); break;
+    case IKL_BF16: e = launch_dim<bf16_tag>(a->head_dim, pl, p, grid, s, a->events); break;
+    default: e = launch_dim<f32_tag>(a->head_dim, pl, p, grid, s, a->events); break;
+  }
+  if (e != hipSuccess) return fail(IKL_ELAUNCH, std::string("paged attention launch: ") + hipGetErrorString(e));
+  return IKL_OK;
+}

@@ -1,0 +1,477 @@
+"""Operator surface of the paged-KV decode path, backed by libikl_paged.so.
+
+Same call signatures, argument meaning and error behaviour as the
+reference's Triton operators:
+
+* :func:`paged_decode_attention_hip` — ``paged_decode_attention_triton``
+  (triton_ops.py:404-478);
+* :func:`paged_decode_attention_hip_grouped` —
+  ``paged_decode_attention_triton_grouped`` (triton_ops.py:481-610);
+* :func:`append_kv_hip` — ``append_kv_triton`` (append.py:69-106);
+* :func:`paged_decode_grouped_path` — ``paged_decode_grouped_path``
+  (triton_ops.py:56-75), answering with this library's kernel families;
+* :func:`hip_available` / :func:`hip_append_available` —
+  ``triton_available`` / ``triton_append_available``.
+
+The ``*_triton`` names are kept as aliases of the same functions so callers
+written against the reference bind unchanged. Every operator launches the
+HIP kernels on the current torch stream and never computes on another path:
+without the built library or a GPU it raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_DTYPES = {
+    torch.float16: _lib.IKL_F16,
+    torch.bfloat16: _lib.IKL_BF16,
+    torch.float32: _lib.IKL_F32,
+}
+_INDEX_TYPES = {torch.int32: _lib.IKL_I32, torch.int64: _lib.IKL_I64}
+
+_PATH_NAMES = {
+    _lib.IKL_PATH_MHA_FALLBACK: "mha_fallback",
+    _lib.IKL_PATH_SCALAR_GROUPED: "scalar_grouped",
+    _lib.IKL_PATH_MFMA_GROUPED: "mfma_grouped",
+}
+_PATH_IDS = {name: ident for ident, name in _PATH_NAMES.items()}
+
+
+def hip_available() -> bool:
+    """True when libikl_paged.so loads and a GPU is visible."""
+    return torch.cuda.is_available() and _lib.library_loaded()
+
+
+def hip_append_available() -> bool:
+    return hip_available()
+
+
+def _require_backend() -> ctypes.CDLL:
+    if not torch.cuda.is_available():
+        raise RuntimeError("HIP paged-decode backend is unavailable: no GPU is visible")
+    try:
+        return _lib.load()
+    except RuntimeError as exc:
+        raise RuntimeError(f"HIP paged-decode backend is unavailable: {exc}") from exc
+
+
+def paged_decode_grouped_path(
+    *,
+    dtype: torch.dtype,
+    head_dim: int,
+    table_width: int,
+    heads_per_kv: int,
+    query_group_size: int,
+) -> str:
+    """Kernel family a grouped launch of this static shape runs.
+
+    ``"mha_fallback"`` when every KV head serves one query head, else
+    ``"scalar_grouped"`` (the query group shares each K/V tile on the VALU).
+    Pure function of its arguments, like triton_ops.py:56-75; the library's
+    ``ikl_paged_attention_path`` applies the same rule.
+    """
+    if heads_per_kv == 1:
+        return "mha_fallback"
+    return "scalar_grouped"
+
+
+def _as_index_tensor(value, device: torch.device) -> torch.Tensor:
+    if isinstance(value, list):
+        return torch.tensor(value, dtype=torch.int32, device=device)
+    return value
+
+
+def _validate_attention(query, cache, block_tables, context_lens, layer, validate_inputs):
+    """Checks of triton_ops.py:415-457, in the same order with the same
+    messages; returns the table and length tensors."""
+    if query.ndim != 3 or query.device.type != "cuda":
+        raise ValueError("query must be a GPU (torch 'cuda' device) tensor with shape [B,H,D]")
+    if query.shape[0] <= 0 or query.shape[1] <= 0 or query.shape[2] <= 0:
+        raise ValueError("query dimensions must be positive")
+    if query.shape[-1] > 128:
+        raise ValueError("the current HIP kernel supports head_dim <= 128")
+    if query.stride(-1) != 1:
+        raise ValueError("query must be contiguous in the head_dim dimension")
+    block_tables = _as_index_tensor(block_tables, query.device)
+    context_lens = _as_index_tensor(context_lens, query.device)
+    layout = cache.layout
+    if not 0 <= layer < layout.num_layers:
+        raise IndexError("layer is out of range")
+    if query.shape[-1] != layout.head_dim:
+        raise ValueError("query head_dim does not match cache layout")
+    if query.shape[1] % layout.num_kv_heads != 0:
+        raise ValueError("num_heads must be divisible by num_kv_heads")
+    if query.dtype != cache.dtype or query.device != cache.device:
+        raise ValueError("query and cache must have the same dtype and device")
+    if block_tables.ndim != 2 or block_tables.shape[0] != query.shape[0]:
+        raise ValueError("block_tables must have shape [B, max_blocks]")
+    if context_lens.ndim != 1 or context_lens.shape[0] != query.shape[0]:
+        raise ValueError("context_lens must have shape [B]")
+    if block_tables.device != query.device or context_lens.device != query.device:
+        raise ValueError("block_tables and context_lens must be on the query device")
+    if block_tables.dtype not in _INDEX_TYPES:
+        raise ValueError("block_tables must use int32 or int64")
+    if context_lens.dtype not in _INDEX_TYPES:
+        raise ValueError("context_lens must use int32 or int64")
+    if block_tables.shape[1] <= 0:
+        raise ValueError("block_tables must contain at least one logical block")
+    if validate_inputs:
+        if bool(torch.any(context_lens <= 0).item()):
+            raise ValueError("context lengths must be positive")
+        max_context = block_tables.shape[1] * layout.block_size
+        if bool(torch.any(context_lens > max_context).item()):
+            raise ValueError("context length exceeds block table capacity")
+        if bool(torch.any(block_tables < 0).item()) or bool(
+            torch.any(block_tables >= layout.num_blocks).item()
+        ):
+            raise ValueError("block table contains an invalid physical block id")
+    if query.dtype not in _DTYPES:
+        raise ValueError("query dtype must be float16, bfloat16 or float32")
+    return block_tables, context_lens
+
+
+def _aligned_rows(t: torch.Tensor) -> bool:
+    vec = 16 // t.element_size()
+    return t.data_ptr() % 16 == 0 and all(s % vec == 0 for s in t.stride()[:-1])
+
+
+def _attention_args(
+    query,
+    cache,
+    block_tables,
+    context_lens,
+    out,
+    scale,
+    layer,
+    query_group_size,
+    partition_size,
+    max_context_len,
+    path,
+):
+    layout = cache.layout
+    k_cache = cache.k[layer]
+    v_cache = cache.v[layer]
+    if block_tables.stride(-1) != 1:
+        block_tables = block_tables.contiguous()
+    if context_lens.stride(0) != 1:
+        context_lens = context_lens.contiguous()
+    args = _lib.PagedAttentionArgs()
+    args.query = query.data_ptr()
+    args.q_stride_b, args.q_stride_h = query.stride(0), query.stride(1)
+    args.k_cache = k_cache.data_ptr()
+    args.v_cache = v_cache.data_ptr()
+    args.k_stride_block, args.k_stride_token, args.k_stride_head = k_cache.stride()[:3]
+    args.v_stride_block, args.v_stride_token, args.v_stride_head = v_cache.stride()[:3]
+    args.block_tables = block_tables.data_ptr()
+    args.table_type = _INDEX_TYPES[block_tables.dtype]
+    args.table_stride_b = block_tables.stride(0)
+    args.table_width = block_tables.shape[1]
+    args.context_lens = context_lens.data_ptr()
+    args.lens_type = _INDEX_TYPES[context_lens.dtype]
+    args.out = out.data_ptr()
+    args.out_stride_b, args.out_stride_h = out.stride(0), out.stride(1)
+    args.batch = query.shape[0]
+    args.num_blocks = layout.num_blocks
+    args.num_heads = query.shape[1]
+    args.num_kv_heads = layout.num_kv_heads
+    args.head_dim = layout.head_dim
+    args.block_size = layout.block_size
+    args.dtype = _DTYPES[query.dtype]
+    args.scale = float(scale if scale is not None else layout.head_dim**-0.5)
+    args.query_group_size = int(query_group_size)
+    args.partition_size = int(partition_size)
+    args.max_context_len = int(max_context_len)
+    args.path = int(path)
+    # keep the tensors whose pointers the struct holds alive with it
+    return args, (block_tables, context_lens, k_cache, v_cache)
+
+
+def _launch_attention(
+    query,
+    cache,
+    block_tables,
+    context_lens,
+    scale,
+    layer,
+    *,
+    query_group_size: int,
+    partition_size: int | None,
+    max_context_len: int | None,
+    path: int = -1,
+    events=None,
+) -> torch.Tensor:
+    lib = _require_backend()
+    if not _aligned_rows(query):
+        query = query.contiguous()
+    for tensor in (cache.k, cache.v):
+        if not _aligned_rows(tensor):
+            raise ValueError("cache tensors must have 16-byte aligned head_dim rows")
+    output = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    args, keep = _attention_args(
+        query,
+        cache,
+        block_tables,
+        context_lens,
+        output,
+        scale,
+        layer,
+        query_group_size,
+        partition_size or 0,
+        max_context_len or 0,
+        path,
+    )
+    ws_bytes = lib.ikl_paged_attention_workspace_size(ctypes.byref(args))
+    _lib.check(ws_bytes if ws_bytes < 0 else 0, "paged attention")
+    workspace = None
+    if ws_bytes > 0:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
+        args.workspace = workspace.data_ptr()
+        args.workspace_bytes = ws_bytes
+    if events is not None:
+        for i, ev in enumerate(events):
+            args.events[i] = ev
+    with torch.cuda.device(query.device):
+        stream = torch.cuda.current_stream(query.device).cuda_stream
+        status = lib.ikl_paged_attention(ctypes.byref(args), ctypes.c_void_p(stream))
+    _lib.check(status, "paged attention")
+    del keep, workspace  # the caching allocator keeps stream order
+    return output
+
+
+def paged_decode_attention_hip(
+    query,
+    cache,
+    block_tables,
+    context_lens,
+    scale=None,
+    layer=0,
+    *,
+    validate_inputs=True,
+    partition_size: int | None = None,
+    max_context_len: int | None = None,
+    events=None,
+):
+    """Paged decode attention; disable value checks only for prevalidated inputs.
+
+    Signature of ``paged_decode_attention_triton`` (triton_ops.py:404-413).
+    All query heads of a KV head share each K/V tile in one workgroup (the
+    kernel family is picked by :func:`paged_decode_grouped_path`). Extra
+    keyword-only knobs: ``partition_size`` (tokens per split-context
+    partition; ``-1`` never splits, ``None`` picks automatically),
+    ``max_context_len`` (a host-known bound of ``context_lens`` used to size
+    the split grid) and ``events`` (up to three raw hipEvent_t handles
+    recorded before the attention kernel, after it and after the split
+    reduce, for timing).
+    """
+    block_tables, context_lens = _validate_attention(
+        query, cache, block_tables, context_lens, layer, validate_inputs
+    )
+    return _launch_attention(
+        query,
+        cache,
+        block_tables,
+        context_lens,
+        scale,
+        layer,
+        query_group_size=0,
+        partition_size=partition_size,
+        max_context_len=max_context_len,
+        events=events,
+    )
+
+
+def paged_decode_attention_hip_grouped(
+    query,
+    cache,
+    block_tables,
+    context_lens,
+    scale=None,
+    layer=0,
+    *,
+    query_group_size=8,
+    validate_inputs=True,
+    partition_size: int | None = None,
+    max_context_len: int | None = None,
+):
+    """Grouped-query paged attention with one K/V tile per query group.
+
+    Signature of ``paged_decode_attention_triton_grouped``
+    (triton_ops.py:481-491): ``min(query_group_size, H/Hkv)`` query heads
+    share each K/V tile; MHA shapes take the one-head path (541-551).
+    """
+    block_tables, context_lens = _validate_attention(
+        query, cache, block_tables, context_lens, layer, validate_inputs
+    )
+    if query_group_size not in (1, 2, 4, 8):
+        raise ValueError("query_group_size must be one of 1, 2, 4, or 8")
+    heads_per_kv = query.shape[1] // cache.layout.num_kv_heads
+    path_name = paged_decode_grouped_path(
+        dtype=query.dtype,
+        head_dim=cache.layout.head_dim,
+        table_width=block_tables.shape[1],
+        heads_per_kv=heads_per_kv,
+        query_group_size=query_group_size,
+    )
+    return _launch_attention(
+        query,
+        cache,
+        block_tables,
+        context_lens,
+        scale,
+        layer,
+        query_group_size=1 if heads_per_kv == 1 else query_group_size,
+        partition_size=partition_size,
+        max_context_len=max_context_len,
+        path=_PATH_IDS[path_name],
+    )
+
+
+def append_kv_hip(key: torch.Tensor, value: torch.Tensor, cache, slots: torch.Tensor, layer: int = 0) -> None:
+    """Append ``[tokens, kv_heads, head_dim]`` rows into paged cache slots.
+
+    Signature and checks of ``append_kv_triton`` (append.py:69-106); writes
+    ``cache.k[layer]`` / ``cache.v[layer]`` in place on the current stream.
+    Slots outside ``[0, num_blocks * block_size)`` are skipped.
+    """
+    lib = _require_backend()
+    if key.shape != value.shape or key.ndim != 3:
+        raise ValueError("key/value must have shape [T, Hkv, D]")
+    if key.device.type != "cuda" or slots.device != key.device or value.device != key.device:
+        raise ValueError("key/value/slots must be on the same GPU device")
+    layout = cache.layout
+    if tuple(key.shape[1:]) != (layout.num_kv_heads, layout.head_dim):
+        raise ValueError("key/value shape does not match cache layout")
+    if slots.numel() != key.shape[0]:
+        raise ValueError("slots and key/value token counts must match")
+    if not 0 <= layer < layout.num_layers:
+        raise IndexError("layer is out of range")
+    if key.dtype != cache.dtype or value.dtype != cache.dtype:
+        raise ValueError("key/value dtype must match the cache dtype")
+    if slots.dtype not in _INDEX_TYPES:
+        raise ValueError("slots must use int32 or int64")
+    if key.stride(-1) != 1:
+        key = key.contiguous()
+    if value.stride(-1) != 1:
+        value = value.contiguous()
+    slots = slots.reshape(-1)
+    if slots.numel() and slots.stride(0) != 1:
+        slots = slots.contiguous()
+    if key.shape[0] == 0:
+        return
+    args, keep = _append_args(key, value, cache, slots, layer)
+    with torch.cuda.device(key.device):
+        stream = torch.cuda.current_stream(key.device).cuda_stream
+        status = lib.ikl_append_kv(ctypes.byref(args), ctypes.c_void_p(stream))
+    del keep
+    _lib.check(status, "append_kv")
+
+
+def _append_args(key, value, cache, slots, layer):
+    layout = cache.layout
+    k_cache = cache.k[layer]
+    v_cache = cache.v[layer]
+    args = _lib.AppendArgs()
+    args.key, args.value = key.data_ptr(), value.data_ptr()
+    args.key_stride_t, args.key_stride_h = key.stride(0), key.stride(1)
+    args.value_stride_t, args.value_stride_h = value.stride(0), value.stride(1)
+    args.slots = slots.data_ptr()
+    args.slot_type = _INDEX_TYPES[slots.dtype]
+    args.k_cache, args.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+    args.k_stride_block, args.k_stride_token, args.k_stride_head = k_cache.stride()[:3]
+    args.v_stride_block, args.v_stride_token, args.v_stride_head = v_cache.stride()[:3]
+    args.num_tokens = key.shape[0]
+    args.num_blocks = layout.num_blocks
+    args.block_size = layout.block_size
+    args.num_kv_heads = layout.num_kv_heads
+    args.head_dim = layout.head_dim
+    args.dtype = _DTYPES[key.dtype]
+    return args, (key, value, slots, k_cache, v_cache)
+
+
+class PreparedPagedAttention:
+    """Paged decode attention validated once on fixed buffers.
+
+    Binds the query, one cache layer, block tables, context lengths, an
+    output buffer and the split workspace; each call only enqueues the
+    kernels on the current stream (no validation, allocation or host sync).
+    Callers may update the bound tensors in place between calls (new query
+    rows, longer contexts up to ``max_context_len``, appended table
+    entries) — the same metadata reuse as the reference's decode loop
+    (decode.py:361-391). Results equal :func:`paged_decode_attention_hip`.
+    """
+
+    def __init__(self, query, cache, block_tables, context_lens, scale=None, layer=0, *,
+                 query_group_size: int = 0, partition_size: int | None = None,
+                 max_context_len: int | None = None, validate_inputs: bool = True):
+        self._lib = _require_backend()
+        block_tables, context_lens = _validate_attention(
+            query, cache, block_tables, context_lens, layer, validate_inputs
+        )
+        if not _aligned_rows(query):
+            raise ValueError("query rows must be 16-byte aligned for a prepared launch")
+        for tensor in (cache.k, cache.v):
+            if not _aligned_rows(tensor):
+                raise ValueError("cache tensors must have 16-byte aligned head_dim rows")
+        self.query = query
+        self.block_tables = block_tables
+        self.context_lens = context_lens
+        self.out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+        self._args, self._keep = _attention_args(
+            query, cache, block_tables, context_lens, self.out, scale, layer, query_group_size,
+            partition_size or 0, max_context_len or 0, -1,
+        )
+        ws = self._lib.ikl_paged_attention_workspace_size(ctypes.byref(self._args))
+        _lib.check(ws if ws < 0 else 0, "paged attention")
+        self.workspace = torch.empty(max(ws, 1), dtype=torch.uint8, device=query.device)
+        self._args.workspace = self.workspace.data_ptr()
+        self._args.workspace_bytes = ws
+        self.partition_size = self._lib.ikl_paged_attention_partition_size(ctypes.byref(self._args))
+        self.device = query.device
+
+    def __call__(self, events=None) -> torch.Tensor:
+        for i in range(3):
+            self._args.events[i] = events[i] if events is not None else None
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        status = self._lib.ikl_paged_attention(ctypes.byref(self._args), ctypes.c_void_p(stream))
+        _lib.check(status, "paged attention")
+        return self.out
+
+
+class PreparedAppend:
+    """KV append validated once on fixed key/value/slot buffers; each call
+    only enqueues the scatter (see :func:`append_kv_hip`)."""
+
+    def __init__(self, key, value, cache, slots, layer: int = 0):
+        self._lib = _require_backend()
+        if key.shape != value.shape or key.ndim != 3 or key.stride(-1) != 1 or value.stride(-1) != 1:
+            raise ValueError("key/value must be [T, Hkv, D] with a contiguous last dimension")
+        if tuple(key.shape[1:]) != (cache.layout.num_kv_heads, cache.layout.head_dim):
+            raise ValueError("key/value shape does not match cache layout")
+        if slots.ndim != 1 or slots.numel() != key.shape[0] or slots.stride(0) != 1:
+            raise ValueError("slots and key/value token counts must match")
+        if slots.dtype not in _INDEX_TYPES:
+            raise ValueError("slots must use int32 or int64")
+        if key.dtype != cache.dtype or value.dtype != cache.dtype:
+            raise ValueError("key/value dtype must match the cache dtype")
+        if not 0 <= layer < cache.layout.num_layers:
+            raise IndexError("layer is out of range")
+        self._args, self._keep = _append_args(key, value, cache, slots, layer)
+        self.device = key.device
+
+    def __call__(self) -> None:
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        status = self._lib.ikl_append_kv(ctypes.byref(self._args), ctypes.c_void_p(stream))
+        _lib.check(status, "append_kv")
+
+
+# Names of the reference's operators, bound to the same HIP functions.
+paged_decode_attention_triton = paged_decode_attention_hip
+paged_decode_attention_triton_grouped = paged_decode_attention_hip_grouped
+append_kv_triton = append_kv_hip
+triton_available = hip_available
+triton_append_available = hip_append_available

@@ -1,0 +1,231 @@
+"""CPU oracle of the paged-KV decode path — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this module, and only as the checker (or as the
+timed CPU baseline); the product path (``inferkernellab_amd``) never routes
+through it.
+
+It restates, in numpy, the reference's algorithm for this path:
+
+* ``OracleCache.slot_mapping``   — cache.py:113-129
+* ``OracleCache.write_slots``    — cache.py:156-189 (torch index_put semantics)
+* ``OracleCache.write``          — cache.py:131-154
+* ``OracleCache.read``           — cache.py:191-200
+* ``expand_kv``                  — attention.py:9-15 (repeat_interleave)
+* ``dense_decode_attention``     — attention.py:18-36 (fp32 einsum/softmax/einsum)
+* ``paged_decode_attention``     — attention.py:134-175 (= backend ``paged_reference``)
+
+Storage keeps the cache's own element type: float16 and float32 as numpy
+arrays of that type, bfloat16 as raw ``uint16`` bit patterns (numpy has no
+bfloat16), so append results can be compared bit for bit. Attention upcasts
+to float32 exactly like ``query.float()`` / ``key.float()`` in the reference
+and returns float32 (the tolerance reference); ``cast_output`` applies the
+reference's final ``.to(query.dtype)``.
+
+Parity pins (each checked in tests/test_oracle.py):
+* slot_mapping / write / read / allocator: the known answers of the
+  reference's tests (tests/golden/known_answers.json, transcribed from
+  tests/test_cache.py:8-84 and tests/test_attention.py:129-144);
+* attention: float64 brute force on tiny inputs, closed forms (context 1 ->
+  v, equal keys -> mean of v, one dominant key -> its v), MHA == GQA after
+  explicit head expansion, block-table permutation invariance, and torch's
+  own softmax/einsum on the same data.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+DTYPES = ("float16", "bfloat16", "float32")
+
+
+# ------------------------------------------------------------ element types
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    """Exact bfloat16 -> float32 widening of raw uint16 bit patterns."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16 bits, round to nearest even (NaN stays NaN)."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, np.uint16(0x7FC0), rounded).astype(np.uint16)
+
+
+def to_f32(storage: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "bfloat16":
+        return bf16_bits_to_f32(storage)
+    return np.asarray(storage).astype(np.float32)
+
+
+def storage_dtype(dtype: str):
+    return {"float16": np.float16, "bfloat16": np.uint16, "float32": np.float32}[dtype]
+
+
+def cast_output(x: np.ndarray, dtype: str) -> np.ndarray:
+    """The reference's ``.to(query.dtype)`` (attention.py:36), as storage."""
+    if dtype == "bfloat16":
+        return f32_to_bf16_bits(x)
+    return np.asarray(x, dtype=np.float32).astype(storage_dtype(dtype))
+
+
+# -------------------------------------------------------------------- cache
+class OracleCache:
+    """Storage ``[layers, blocks, block_size, kv_heads, head_dim]`` (cache.py:90)."""
+
+    def __init__(self, num_blocks, block_size, num_kv_heads, head_dim, *, num_layers=1,
+                 dtype="float32", fill=np.nan):
+        if min(num_layers, num_blocks, block_size, num_kv_heads, head_dim) <= 0:
+            raise ValueError("cache dimensions must be positive")
+        if dtype not in DTYPES:
+            raise ValueError(f"unsupported dtype {dtype}")
+        self.num_layers = num_layers
+        self.num_blocks = num_blocks
+        self.block_size = block_size
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.dtype = dtype
+        shape = (num_layers, num_blocks, block_size, num_kv_heads, head_dim)
+        sd = storage_dtype(dtype)
+        if dtype == "bfloat16":
+            init = f32_to_bf16_bits(np.float32(fill))
+        else:
+            init = sd(fill)
+        self.k = np.full(shape, init, dtype=sd)
+        self.v = np.full(shape, init, dtype=sd)
+
+    def slot_mapping(self, block_table, start: int, length: int) -> np.ndarray:
+        """slot(p) = table[p // bs] * bs + p % bs for p in [start, start+length)."""
+        if start < 0 or length < 0:
+            raise ValueError("start and length must be non-negative")
+        table = list(block_table)
+        if any(not isinstance(b, (int, np.integer)) or not 0 <= int(b) < self.num_blocks for b in table):
+            raise ValueError("block_table contains an invalid physical block id")
+        if length and (start + length - 1) // self.block_size >= len(table):
+            raise ValueError("block_table is shorter than the requested range")
+        out = np.empty(length, dtype=np.int64)
+        for i, p in enumerate(range(start, start + length)):
+            out[i] = int(table[p // self.block_size]) * self.block_size + p % self.block_size
+        return out
+
+    def write_slots(self, layer: int, slots, key: np.ndarray, value: np.ndarray, *,
+                    validate_slots: bool = True) -> None:
+        """k[layer, slot // bs, slot % bs, :, :] = key[t] for every token t."""
+        key = np.asarray(key)
+        value = np.asarray(value)
+        slots = np.asarray(slots, dtype=np.int64).reshape(-1)
+        if key.shape != value.shape or key.ndim != 3:
+            raise ValueError("key/value must have the same [T, H, D] shape")
+        if slots.shape[0] != key.shape[0]:
+            raise ValueError("slots must have one entry per key/value token")
+        if key.shape[1:] != (self.num_kv_heads, self.head_dim):
+            raise ValueError("key/value shape does not match cache layout")
+        if not 0 <= layer < self.num_layers:
+            raise IndexError("layer is out of range")
+        limit = self.num_blocks * self.block_size
+        if validate_slots and slots.size and (slots.min() < 0 or slots.max() >= limit):
+            raise ValueError("slots contain an invalid physical cache position")
+        # numpy fancy assignment: with duplicate slots the last row wins (the
+        # reference's torch index_put leaves that order unspecified)
+        blocks, offsets = slots // self.block_size, slots % self.block_size
+        self.k[layer, blocks, offsets] = key
+        self.v[layer, blocks, offsets] = value
+
+    def write(self, layer: int, block_table, start: int, key, value) -> None:
+        key = np.asarray(key)
+        if key.ndim != 3:
+            raise ValueError("key/value must have the same [T, H, D] shape")
+        slots = self.slot_mapping(block_table, start, key.shape[0])
+        self.write_slots(layer, slots, key, value, validate_slots=False)
+
+    def read(self, layer: int, block_table, length: int):
+        """First ``length`` logical tokens in order, as storage arrays."""
+        if length < 0:
+            raise ValueError("length must be non-negative")
+        slots = self.slot_mapping(block_table, 0, length)
+        if not 0 <= layer < self.num_layers:
+            raise IndexError("layer is out of range")
+        blocks = slots // self.block_size
+        offsets = slots % self.block_size
+        return self.k[layer, blocks, offsets], self.v[layer, blocks, offsets]
+
+
+# ---------------------------------------------------------------- attention
+def expand_kv(x: np.ndarray, num_heads: int) -> np.ndarray:
+    """[T, Hkv, D] -> [T, H, D]; query head h reads kv head h // (H // Hkv)."""
+    if x.shape[1] == num_heads:
+        return x
+    if num_heads % x.shape[1] != 0:
+        raise ValueError("num_heads must be divisible by num_kv_heads")
+    return np.repeat(x, num_heads // x.shape[1], axis=1)
+
+
+def dense_decode_attention(query: np.ndarray, key: np.ndarray, value: np.ndarray, *,
+                           scale: float | None = None) -> np.ndarray:
+    """fp32 softmax(q.k * scale) @ v for q [B,H,D], k/v [T,Hkv,D] -> [B,H,D] fp32."""
+    if query.ndim != 3 or key.ndim != 3 or value.ndim != 3:
+        raise ValueError("query must be [B,H,D], key/value must be [T,Hkv,D]")
+    if key.shape != value.shape or query.shape[2] != key.shape[2]:
+        raise ValueError("incompatible attention shapes")
+    q = np.asarray(query, dtype=np.float32)
+    k = expand_kv(np.asarray(key, dtype=np.float32), q.shape[1]).transpose(1, 0, 2)  # [H,T,D]
+    v = expand_kv(np.asarray(value, dtype=np.float32), q.shape[1]).transpose(1, 0, 2)
+    scores = np.einsum("bhd,htd->bht", q, k, optimize=True).astype(np.float32)
+    scores *= np.float32(scale if scale is not None else q.shape[-1] ** -0.5)
+    scores -= scores.max(axis=-1, keepdims=True)
+    probs = np.exp(scores, dtype=np.float32)
+    probs /= probs.sum(axis=-1, keepdims=True)
+    return np.einsum("bht,htd->bhd", probs, v, optimize=True).astype(np.float32)
+
+
+def paged_decode_attention(query_f32: np.ndarray, cache: OracleCache, block_tables,
+                           context_lens, *, scale: float | None = None,
+                           layer: int = 0) -> np.ndarray:
+    """Per-request loop: gather the first ctx tokens through the block table,
+    then dense fp32 attention (attention.py:134-175). Returns fp32 [B,H,D]."""
+    query_f32 = np.asarray(query_f32, dtype=np.float32)
+    if query_f32.ndim != 3:
+        raise ValueError("query must be [B,H,D]")
+    batch, num_heads, head_dim = query_f32.shape
+    if head_dim != cache.head_dim:
+        raise ValueError("query head_dim does not match cache")
+    if num_heads % cache.num_kv_heads != 0:
+        raise ValueError("num_heads must be divisible by num_kv_heads")
+    lengths = [int(x) for x in np.asarray(context_lens).reshape(-1)]
+    tables = [list(map(int, row)) for row in block_tables]
+    if len(lengths) != batch:
+        raise ValueError("context_lens must have one entry per query")
+    if len(tables) != batch:
+        raise ValueError("block_tables must have one row per query")
+    outputs = np.empty((batch, num_heads, head_dim), dtype=np.float32)
+    for index, length in enumerate(lengths):
+        if length <= 0:
+            raise ValueError("context lengths must be positive")
+        k_raw, v_raw = cache.read(layer, tables[index], length)
+        k = to_f32(k_raw, cache.dtype)
+        v = to_f32(v_raw, cache.dtype)
+        outputs[index] = dense_decode_attention(query_f32[index:index + 1], k, v, scale=scale)[0]
+    return outputs
+
+
+def brute_force_attention_f64(query, keys, values, *, scale=None):
+    """Pure-Python float64 attention for tiny inputs: q [H][D], keys/values
+    [T][Hkv][D] nested lists; returns [H][D]. Independent of numpy."""
+    num_heads = len(query)
+    num_kv = len(keys[0])
+    group = num_heads // num_kv
+    head_dim = len(query[0])
+    s = scale if scale is not None else head_dim ** -0.5
+    out = []
+    for h in range(num_heads):
+        kvh = h // group
+        scores = [s * sum(query[h][d] * keys[t][kvh][d] for d in range(head_dim)) for t in range(len(keys))]
+        mx = max(scores)
+        weights = [math.exp(x - mx) for x in scores]
+        z = sum(weights)
+        out.append([sum(weights[t] * values[t][kvh][d] for t in range(len(keys))) / z
+                    for d in range(head_dim)])
+    return out

@@ -1,0 +1,134 @@
+"""Shared builders for the parity tests: seeded inputs written into the
+oracle cache, then copied bit for bit into the product's device cache."""
+
+from __future__ import annotations
+
+import json
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from oracle import paged_oracle as po
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+TORCH_DTYPES = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}
+# Tolerances stated for this path: max-abs vs the fp32 oracle.
+ATOL = {"float16": 2e-3, "bfloat16": 1e-2, "float32": 1e-4}
+
+
+def known_answers() -> dict:
+    return json.loads((GOLDEN / "known_answers.json").read_text())
+
+
+def storage_to_torch(arr: np.ndarray, dtype: str) -> torch.Tensor:
+    """numpy storage (bf16 as uint16 bits) -> torch tensor of `dtype`, same bits."""
+    arr = np.ascontiguousarray(arr)
+    if dtype == "bfloat16":
+        return torch.from_numpy(arr.view(np.int16)).view(torch.bfloat16)
+    return torch.from_numpy(arr)
+
+
+def torch_to_storage(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def randn_storage(gen: torch.Generator, shape, dtype: str, scale: float = 1.0) -> np.ndarray:
+    x = torch.randn(shape, generator=gen, dtype=torch.float32) * scale
+    return torch_to_storage(x.to(TORCH_DTYPES[dtype]))
+
+
+@dataclass
+class Case:
+    dtype: str
+    oracle_cache: po.OracleCache
+    query: np.ndarray  # storage
+    tables: list[list[int]]
+    lengths: list[int]
+    num_heads: int
+
+    @property
+    def query_f32(self) -> np.ndarray:
+        return po.to_f32(self.query, self.dtype)
+
+    def expected(self, scale=None, layer=0) -> np.ndarray:
+        return po.paged_decode_attention(
+            self.query_f32, self.oracle_cache, self.tables, self.lengths, scale=scale, layer=layer
+        )
+
+    def device_cache(self, device="cuda"):
+        from inferkernellab_amd.cache import PagedKVCache
+
+        oc = self.oracle_cache
+        cache = PagedKVCache(
+            oc.num_blocks,
+            oc.block_size,
+            oc.num_kv_heads,
+            oc.head_dim,
+            num_layers=oc.num_layers,
+            dtype=TORCH_DTYPES[self.dtype],
+            device=device,
+        )
+        cache.k.copy_(storage_to_torch(oc.k, self.dtype))
+        cache.v.copy_(storage_to_torch(oc.v, self.dtype))
+        return cache
+
+    def device_query(self, device="cuda") -> torch.Tensor:
+        return storage_to_torch(self.query, self.dtype).to(device)
+
+    def device_tables(self, device="cuda", dtype=torch.int32) -> torch.Tensor:
+        width = max(len(t) for t in self.tables)
+        padded = [list(t) + [0] * (width - len(t)) for t in self.tables]
+        return torch.tensor(padded, dtype=dtype, device=device)
+
+    def device_lengths(self, device="cuda", dtype=torch.int32) -> torch.Tensor:
+        return torch.tensor(self.lengths, dtype=dtype, device=device)
+
+
+def make_case(
+    *,
+    batch: int,
+    num_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    block_size: int,
+    lengths,
+    dtype: str,
+    seed: int = 0,
+    num_blocks: int | None = None,
+    num_layers: int = 1,
+    layer: int = 0,
+    kv_scale: float = 1.0,
+    poison=np.nan,
+) -> Case:
+    """Random permutation block tables drawn from a pool; K/V ~ N(0,1)*kv_scale
+    written through slot_mapping; unwritten slots hold `poison`."""
+    lengths = [int(x) for x in lengths]
+    assert len(lengths) == batch
+    need = [-(-n // block_size) for n in lengths]
+    pool = num_blocks if num_blocks is not None else sum(need) + 8
+    gen = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(pool, generator=gen).tolist()
+    tables, used = [], 0
+    for n in need:
+        tables.append(perm[used : used + n])
+        used += n
+    cache = po.OracleCache(pool, block_size, num_kv_heads, head_dim, num_layers=num_layers,
+                           dtype=dtype, fill=poison)
+    for table, n in zip(tables, lengths):
+        key = randn_storage(gen, (n, num_kv_heads, head_dim), dtype, kv_scale)
+        value = randn_storage(gen, (n, num_kv_heads, head_dim), dtype, kv_scale)
+        slots = cache.slot_mapping(table, 0, n)
+        cache.write_slots(layer, slots, key, value)
+    query = randn_storage(gen, (batch, num_heads, head_dim), dtype)
+    return Case(dtype, cache, query, tables, lengths, num_heads)
+
+
+def max_abs_err(actual: torch.Tensor, expected: np.ndarray) -> float:
+    a = actual.detach().float().cpu().numpy()
+    return float(np.max(np.abs(a - expected)))

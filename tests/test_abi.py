@@ -1,0 +1,120 @@
+"""The C-ABI library loads on the CPU host and exports every symbol that
+include/ikl_paged.h declares; its pure host functions (path selection,
+workspace and partition planning) behave as documented. No kernels run."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from inferkernellab_amd import _lib, ops
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "ikl_paged.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ikl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_what_python_binds():
+    assert _declared_functions() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.ikl_version().decode().startswith("ikl_paged")
+
+
+def test_struct_layouts_match_header_field_order():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    for struct_name, cls in (("ikl_append_args", _lib.AppendArgs),
+                             ("ikl_paged_attention_args", _lib.PagedAttentionArgs)):
+        body = re.search(r"typedef struct %s \{(.*?)\}" % struct_name, text, flags=re.S).group(1)
+        fields = []
+        for decl in body.split(";"):
+            decl = decl.strip()
+            if not decl:
+                continue
+            names = decl.split(None, 1)[1] if not decl.startswith("const") else decl.split(None, 2)[2]
+            for name in names.split(","):
+                fields.append(re.sub(r"[\s*]|\[\d+\]", "", name))
+        assert fields == [f[0] for f in cls._fields_], struct_name
+
+
+def _args(**kw):
+    a = _lib.PagedAttentionArgs()
+    a.batch, a.num_heads, a.num_kv_heads, a.head_dim = 32, 32, 8, 128
+    a.block_size, a.num_blocks, a.table_width = 16, 20000, 513
+    a.table_type = a.lens_type = _lib.IKL_I32
+    a.dtype = _lib.IKL_BF16
+    a.path = -1
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_partition_planning_for_the_gqa_decode_shape():
+    lib = _lib.load()
+    a = _args(partition_size=512, max_context_len=8192)
+    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 512
+    ws = lib.ikl_paged_attention_workspace_size(ctypes.byref(a))
+    rows = 32 * 32 * 16
+    assert ws >= rows * 128 * 4 + rows * 4
+    # never split
+    a = _args(partition_size=-1, max_context_len=8192)
+    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 0
+    assert lib.ikl_paged_attention_workspace_size(ctypes.byref(a)) == 0
+    # automatic: short contexts with few workgroups shrink the partition
+    a = _args(partition_size=0, max_context_len=512, batch=16, num_kv_heads=32)
+    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 128
+
+
+def test_invalid_arguments_report_errors():
+    lib = _lib.load()
+    a = _args(num_heads=30)
+    assert lib.ikl_paged_attention_workspace_size(ctypes.byref(a)) == _lib.IKL_EINVAL
+    assert "divisible" in _lib.last_error()
+    a = _args(head_dim=200)
+    assert lib.ikl_paged_attention_workspace_size(ctypes.byref(a)) == _lib.IKL_EUNSUPPORTED
+    a = _args(partition_size=100)
+    assert lib.ikl_paged_attention_workspace_size(ctypes.byref(a)) == _lib.IKL_EINVAL
+    assert "multiple of 64" in _lib.last_error()
+
+
+@pytest.mark.parametrize(
+    ("dtype", "table_width", "heads_per_kv", "expected"),
+    [
+        (torch.float16, 8, 4, "scalar_grouped"),
+        (torch.bfloat16, 16, 32, "scalar_grouped"),
+        (torch.float16, 17, 32, "scalar_grouped"),
+        (torch.float32, 8, 32, "scalar_grouped"),
+        (torch.float16, 8, 1, "mha_fallback"),
+    ],
+)
+def test_grouped_path_truth_table_matches_library(dtype, table_width, heads_per_kv, expected):
+    """Same cases as tests/test_attention.py:22-42, answered with this
+    library's families; the Python selector and the C one agree."""
+    got = ops.paged_decode_grouped_path(dtype=dtype, head_dim=64, table_width=table_width,
+                                        heads_per_kv=heads_per_kv, query_group_size=8)
+    assert got == expected
+    code = _lib.load().ikl_paged_attention_path(ops._DTYPES[dtype], 64, table_width, heads_per_kv, 8)
+    assert ops._PATH_NAMES[code] == expected
+
+
+def test_operators_fail_loudly_without_a_gpu():
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    from inferkernellab_amd import PagedKVCache
+
+    cache = PagedKVCache(4, 4, 1, 16, dtype=torch.float16)
+    key = torch.zeros(1, 1, 16, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="unavailable"):
+        ops.append_kv_hip(key, key, cache, torch.zeros(1, dtype=torch.int32))
+    assert not ops.hip_available()
+    assert ops.triton_available is ops.hip_available

@@ -1,0 +1,177 @@
+"""Paged decode attention through the C ABI vs the fp32 oracle
+(paged_reference, attention.py:134-175). Tolerance: max-abs 2e-3 fp16,
+1e-2 bf16, 1e-4 fp32 against the fp32 result."""
+
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import ATOL, known_answers, make_case, max_abs_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(case, fn, *, label, scale=None, layer=0, **kw):
+    from inferkernellab_amd import ops
+
+    print(f"attention case {label} dtype={case.dtype} H={case.num_heads} "
+          f"Hkv={case.oracle_cache.num_kv_heads} D={case.oracle_cache.head_dim} "
+          f"bs={case.oracle_cache.block_size} lens={case.lengths[:8]} kw={kw}", flush=True)
+    cache = case.device_cache()
+    out = getattr(ops, fn)(case.device_query(), cache, case.device_tables(), case.device_lengths(),
+                           scale=scale, layer=layer, **kw)
+    torch.cuda.synchronize()
+    expected = case.expected(scale=scale, layer=layer)
+    err = max_abs_err(out, expected)
+    assert out.dtype == cache.dtype and out.shape == tuple(case.query.shape)
+    assert err <= ATOL[case.dtype], f"{label}: max abs err {err}"
+    return out
+
+
+@pytest.mark.parametrize("num_kv_heads", [4, 2, 1])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16", "float32"])
+def test_reference_shape_matches_oracle(num_kv_heads, dtype):
+    """The shape of tests/test_attention.py:119-137 (tables [[13,2,9],[5,14,1]], lens 19/23)."""
+    spec = known_answers()["attention_shapes"]["triton_vs_reference"]
+    case = make_case(batch=2, num_heads=4, num_kv_heads=num_kv_heads, head_dim=16, block_size=8,
+                     lengths=spec["lengths"], dtype=dtype, seed=1, num_blocks=16)
+    _check(case, "paged_decode_attention_hip", label="ref-shape")
+
+
+@pytest.mark.parametrize("num_kv_heads", [8, 4, 1])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_grouped_reference_shape(num_kv_heads, dtype):
+    """tests/test_attention.py:140-173: 32 heads, layer 1 of 2, query_group_size 8."""
+    case = make_case(batch=2, num_heads=32, num_kv_heads=num_kv_heads, head_dim=16, block_size=8,
+                     lengths=[19, 23], dtype=dtype, seed=7, num_blocks=32, num_layers=2, layer=1)
+    _check(case, "paged_decode_attention_hip_grouped", label="grouped-ref", layer=1, query_group_size=8)
+
+
+@pytest.mark.parametrize("query_group_size", [1, 2, 4, 8])
+def test_grouped_query_group_sizes(query_group_size):
+    case = make_case(batch=3, num_heads=12, num_kv_heads=2, head_dim=64, block_size=16,
+                     lengths=[100, 7, 333], dtype="bfloat16", seed=20)
+    _check(case, "paged_decode_attention_hip_grouped", label="qgs", query_group_size=query_group_size)
+
+
+@pytest.mark.parametrize("head_dim", [16, 32, 64, 96, 128])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16", "float32"])
+def test_head_dims(head_dim, dtype):
+    case = make_case(batch=3, num_heads=8, num_kv_heads=2, head_dim=head_dim, block_size=16,
+                     lengths=[1, 77, 301], dtype=dtype, seed=head_dim)
+    _check(case, "paged_decode_attention_hip", label="head-dim")
+
+
+@pytest.mark.parametrize("block_size", [1, 4, 8, 16, 32, 5])
+def test_block_sizes(block_size):
+    case = make_case(batch=2, num_heads=8, num_kv_heads=8, head_dim=128, block_size=block_size,
+                     lengths=[250, 1029], dtype="bfloat16", seed=block_size)
+    _check(case, "paged_decode_attention_hip", label="block-size")
+
+
+@pytest.mark.parametrize("partition_size", [-1, 64, 128, 512])
+def test_split_partitions_match(partition_size):
+    case = make_case(batch=4, num_heads=32, num_kv_heads=8, head_dim=128, block_size=16,
+                     lengths=[1, 511, 512, 2049], dtype="bfloat16", seed=30)
+    _check(case, "paged_decode_attention_hip", label="split", partition_size=partition_size)
+
+
+def test_mqa_group_32_bf16():
+    case = make_case(batch=4, num_heads=32, num_kv_heads=1, head_dim=128, block_size=16,
+                     lengths=[1024, 4096, 1500, 3333], dtype="bfloat16", seed=31, kv_scale=0.5)
+    _check(case, "paged_decode_attention_hip", label="mqa")
+
+
+def test_mha_fp16_with_split():
+    case = make_case(batch=4, num_heads=32, num_kv_heads=32, head_dim=128, block_size=16,
+                     lengths=[512] * 4, dtype="float16", seed=32)
+    _check(case, "paged_decode_attention_hip", label="mha", partition_size=128)
+
+
+def test_custom_scale_and_int64_metadata():
+    from inferkernellab_amd import ops
+
+    case = make_case(batch=2, num_heads=8, num_kv_heads=2, head_dim=64, block_size=16,
+                     lengths=[40, 90], dtype="float16", seed=33)
+    cache = case.device_cache()
+    out = ops.paged_decode_attention_hip(case.device_query(), cache, case.device_tables(dtype=torch.int64),
+                                         case.device_lengths(dtype=torch.int64), scale=0.05)
+    torch.cuda.synchronize()
+    assert max_abs_err(out, case.expected(scale=0.05)) <= ATOL["float16"]
+
+
+def test_list_metadata_is_accepted():
+    from inferkernellab_amd import ops
+
+    case = make_case(batch=2, num_heads=4, num_kv_heads=2, head_dim=32, block_size=4,
+                     lengths=[5, 7], dtype="float32", seed=3)
+    cache = case.device_cache()
+    width = max(len(t) for t in case.tables)
+    tables = [t + [0] * (width - len(t)) for t in case.tables]
+    out = ops.paged_decode_attention_hip(case.device_query(), cache, tables, case.lengths)
+    torch.cuda.synchronize()
+    assert max_abs_err(out, case.expected()) <= ATOL["float32"]
+
+
+def test_nan_poisoned_unread_slots_do_not_leak():
+    """Like tests/test_hf_benchmark.py:116-117: unread slots full of NaN."""
+    case = make_case(batch=3, num_heads=16, num_kv_heads=4, head_dim=128, block_size=16,
+                     lengths=[3, 17, 45], dtype="bfloat16", seed=34, poison=np.nan)
+    assert (case.oracle_cache.k == 0x7FC0).any()  # bf16 NaN bits in the unread tails
+    out = _check(case, "paged_decode_attention_hip", label="nan-poison")
+    assert torch.isfinite(out).all()
+
+
+def test_invalid_block_ids_are_masked_without_validation():
+    """validate_inputs=False: ids outside the cache are masked (triton_ops.py:138)."""
+    from inferkernellab_amd import ops
+    from oracle import paged_oracle as po
+
+    case = make_case(batch=1, num_heads=4, num_kv_heads=1, head_dim=64, block_size=16,
+                     lengths=[48], dtype="float32", seed=35)
+    cache = case.device_cache()
+    table = list(case.tables[0])
+    table[1] = 10_000  # the middle block is invalid -> its 16 tokens are masked
+    out = ops.paged_decode_attention_hip(case.device_query(), cache,
+                                         torch.tensor([table], dtype=torch.int32, device="cuda"),
+                                         case.device_lengths(), validate_inputs=False)
+    torch.cuda.synchronize()
+    oc = case.oracle_cache
+    k_all, v_all = oc.read(0, case.tables[0], 48)
+    keep = np.r_[0:16, 32:48]
+    ref = po.dense_decode_attention(case.query_f32, k_all[keep], v_all[keep])
+    assert max_abs_err(out, ref) <= ATOL["float32"]
+
+
+def test_validation_messages_match_reference():
+    """tests/test_attention.py:176-193."""
+    from inferkernellab_amd import PagedKVCache, ops
+
+    cache = PagedKVCache(8, 8, 2, 16, dtype=torch.float16, device="cuda")
+    query = torch.randn(1, 4, 16, device="cuda", dtype=torch.float16)
+    with pytest.raises(ValueError, match="positive"):
+        ops.paged_decode_attention_hip(query, cache, torch.tensor([[0]], dtype=torch.int32, device="cuda"),
+                                       torch.tensor([0], dtype=torch.int32, device="cuda"))
+    with pytest.raises(ValueError, match="physical block"):
+        ops.paged_decode_attention_hip(query, cache, torch.tensor([[8]], dtype=torch.int32, device="cuda"),
+                                       torch.tensor([1], dtype=torch.int32, device="cuda"))
+    with pytest.raises(ValueError, match="capacity"):
+        ops.paged_decode_attention_hip(query, cache, torch.tensor([[0]], dtype=torch.int32, device="cuda"),
+                                       torch.tensor([9], dtype=torch.int32, device="cuda"))
+    with pytest.raises(ValueError, match="query_group_size"):
+        ops.paged_decode_attention_hip_grouped(query, cache, [[0]], [1], query_group_size=3)
+    with pytest.raises(IndexError, match="layer"):
+        ops.paged_decode_attention_hip(query, cache, [[0]], [1], layer=1)
+
+
+def test_repeat_runs_are_bit_identical():
+    from inferkernellab_amd import ops
+
+    case = make_case(batch=4, num_heads=32, num_kv_heads=8, head_dim=128, block_size=16,
+                     lengths=[700, 1500, 64, 3000], dtype="bfloat16", seed=36)
+    cache = case.device_cache()
+    args = (case.device_query(), cache, case.device_tables(), case.device_lengths())
+    a = ops.paged_decode_attention_hip(*args)
+    b = ops.paged_decode_attention_hip(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
