@@ -158,9 +158,16 @@ int ikl_paged_attention(const ikl_paged_attention_args *args, void *stream);
 
 /* Static path selection for a grouped launch; mirrors the role of
  * paged_decode_grouped_path (triton_ops.py:56-75) for this library's
- * kernel families. dtype: enum ikl_dtype. Returns enum ikl_attention_path. */
-int32_t ikl_paged_attention_path(int32_t dtype, int32_t head_dim, int64_t table_width,
-                                 int32_t heads_per_kv, int32_t query_group_size);
+ * kernel families: MHA (heads_per_kv == 1) -> IKL_PATH_MHA_FALLBACK;
+ * fp16/bf16 with head_dim in {32, 64, 96, 128} and block_size a multiple of
+ * 16 -> IKL_PATH_MFMA_GROUPED; otherwise IKL_PATH_SCALAR_GROUPED. The
+ * reference's selector has no block_size argument; this one needs it
+ * because the MFMA tiles assume 16-token block alignment. table_width does
+ * not influence the choice (the MFMA path has no context-length limit).
+ * dtype: enum ikl_dtype. Returns enum ikl_attention_path. */
+int32_t ikl_paged_attention_path(int32_t dtype, int32_t head_dim, int32_t block_size,
+                                 int64_t table_width, int32_t heads_per_kv,
+                                 int32_t query_group_size);
 
 #ifdef __cplusplus
 }

@@ -128,7 +128,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ikl_paged_attention.restype = ctypes.c_int
     lib.ikl_paged_attention.argtypes = [ctypes.POINTER(PagedAttentionArgs), _c_ptr]
     lib.ikl_paged_attention_path.restype = _c_i32
-    lib.ikl_paged_attention_path.argtypes = [_c_i32, _c_i32, _c_i64, _c_i32, _c_i32]
+    lib.ikl_paged_attention_path.argtypes = [_c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32]
 
 
 def load() -> ctypes.CDLL:

@@ -112,6 +112,27 @@ struct alignas(16) u32x4 {
 __device__ inline u32x4 load16(const void *p) {
   return *reinterpret_cast<const u32x4 *>(p);
 }
+
+// 16-byte load through the global address space (global_load_dwordx4,
+// counted by vmcnt only — a generic pointer would become a flat load that
+// also holds lgkmcnt).
+typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) v4u32 *global_v4u32_ptr;
+__device__ inline u32x4 load16_global(const void *p) {
+  const v4u32 v = *(global_v4u32_ptr)(p);
+  return u32x4{v.x, v.y, v.z, v.w};
+}
+__device__ inline v4u32 load16v_global(const void *p) { return *(global_v4u32_ptr)(p); }
+
+// Streaming (non-temporal) 16-byte load for K/V rows that are read exactly
+// once per launch: keeps them from displacing reusable lines in L2 / MALL.
+__device__ inline v4u32 load16v_stream(const void *p) {
+  return __builtin_nontemporal_load((global_v4u32_ptr)(p));
+}
+__device__ inline u32x4 load16_stream(const void *p) {
+  const v4u32 v = load16v_stream(p);
+  return u32x4{v.x, v.y, v.z, v.w};
+}
 __device__ inline void store16(void *p, const u32x4 &v) {
   *reinterpret_cast<u32x4 *>(p) = v;
 }

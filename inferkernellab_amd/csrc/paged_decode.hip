@@ -30,43 +30,10 @@
 #include <string>
 
 #include "ikl_common.h"
+#include "paged_attn.h"
 
 namespace ikl {
 namespace {
-
-constexpr float LOG2E = 1.4426950408889634f;
-constexpr float NEG_SENTINEL = -1.0e30f;  // finite "minus infinity" for running maxima
-constexpr float RESCALE_LOG2 = 8.0f;      // lazy-rescale threshold (factor 256)
-
-struct AttnParams {
-  const char *q;
-  int64_t q_sb, q_sh;  // elements
-  const char *kc;
-  const char *vc;
-  int64_t k_sb, k_st, k_sh;  // elements
-  int64_t v_sb, v_st, v_sh;  // elements
-  const void *tables;
-  int64_t t_sb;
-  int64_t table_width;
-  const void *lens;
-  char *out;
-  int64_t o_sb, o_sh;  // elements
-  float *part_o;       // [B, H, NP, D] fp32 (split only)
-  float *part_lse;     // [B, H, NP] fp32, log2 domain (split only)
-  int64_t num_blocks;
-  int32_t num_heads;
-  int32_t heads_per_kv;
-  int32_t group_size;
-  int32_t groups_per_kv;
-  int32_t block_size;
-  int32_t bs_shift;        // log2(block_size) or -1
-  int32_t partition_size;  // tokens per grid.x slot
-  int32_t num_parts;       // NP (grid.x)
-  int32_t split;           // write partials instead of the output
-  int32_t table_i64;
-  int32_t lens_i64;
-  float scale_log2;        // scale * log2(e)
-};
 
 constexpr int pow2_divisor(int n, int cap) {
   int t = 1;
@@ -74,66 +41,38 @@ constexpr int pow2_divisor(int n, int cap) {
   return t;
 }
 
+constexpr int cmin(int a, int b) { return a < b ? a : b; }
+
+// Tuning knobs (compile-time): lanes per token cap for groups of <= 4 and
+// >= 8 heads, and 16-byte K (and V) loads per lane per tile.
+#ifndef IKL_TPT_CAP_SMALL_GROUP
+#define IKL_TPT_CAP_SMALL_GROUP 8
+#endif
+#ifndef IKL_TPT_CAP_LARGE_GROUP
+#define IKL_TPT_CAP_LARGE_GROUP 16
+#endif
+#ifndef IKL_LOADS_PER_LANE
+#define IKL_LOADS_PER_LANE 4
+#endif
+
 template <typename Tag, int D, int G>
 struct ScalarCfg {
   static constexpr int EB = elem<Tag>::bytes;
   static constexpr int VEC = 16 / EB;              // elements per 16-byte chunk
   static constexpr int NCHUNK = D / VEC;           // chunks per head_dim row
   static_assert(D % VEC == 0, "head_dim must be a multiple of a 16-byte chunk");
-  static constexpr int TPT = pow2_divisor(NCHUNK, G >= 8 ? 16 : 8);  // lanes per token
+  static constexpr int TPT =
+      pow2_divisor(NCHUNK, G >= 8 ? IKL_TPT_CAP_LARGE_GROUP : IKL_TPT_CAP_SMALL_GROUP);
   static constexpr int CPL = NCHUNK / TPT;         // chunks per lane
   static constexpr int LD = CPL * VEC;             // dims per lane
   static constexpr int ROWS = 64 / TPT;            // tokens per row-step
-  static constexpr int R = CPL >= 4 ? 1 : 4 / CPL; // row-steps per tile
-  static constexpr int TI = ROWS * R;              // tokens per tile
+  // Row-steps per tile: IKL_LOADS_PER_LANE chunks of K per lane, and never
+  // more than 64 tokens so one 64-entry block-table window covers a tile.
+  static constexpr int R0 = CPL >= IKL_LOADS_PER_LANE ? 1 : IKL_LOADS_PER_LANE / CPL;
+  static constexpr int R = cmin(R0, 64 / ROWS);
+  static constexpr int TI = ROWS * R;              // tokens per tile (<= 64)
+  static_assert(TI <= 64, "a tile must fit one table window");
 };
-
-__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-template <typename Tag>
-__device__ inline void store_out_chunk(char *dst, const float *v);
-
-template <>
-__device__ inline void store_out_chunk<bf16_tag>(char *dst, const float *v) {
-  u32x4 w;
-  w.x = elem<bf16_tag>::pack2(v[0], v[1]);
-  w.y = elem<bf16_tag>::pack2(v[2], v[3]);
-  w.z = elem<bf16_tag>::pack2(v[4], v[5]);
-  w.w = elem<bf16_tag>::pack2(v[6], v[7]);
-  store16(dst, w);
-}
-template <>
-__device__ inline void store_out_chunk<f16_tag>(char *dst, const float *v) {
-  u32x4 w;
-  w.x = elem<f16_tag>::pack2(v[0], v[1]);
-  w.y = elem<f16_tag>::pack2(v[2], v[3]);
-  w.z = elem<f16_tag>::pack2(v[4], v[5]);
-  w.w = elem<f16_tag>::pack2(v[6], v[7]);
-  store16(dst, w);
-}
-template <>
-__device__ inline void store_out_chunk<f32_tag>(char *dst, const float *v) {
-  u32x4 w;
-  w.x = __float_as_uint(v[0]);
-  w.y = __float_as_uint(v[1]);
-  w.z = __float_as_uint(v[2]);
-  w.w = __float_as_uint(v[3]);
-  store16(dst, w);
-}
-
-// Loads the window of 64 block-table entries starting at logical block
-// `base`; entries outside the table or naming a block outside the cache
-// become -1 (masked).
-__device__ inline int load_table_window(const AttnParams &p, int64_t b, int64_t base, int lane) {
-  const int64_t lb = base + lane;
-  int phys = -1;
-  if (lb < p.table_width) {
-    const int64_t e = p.table_i64 ? load_index<int64_t>(p.tables, b * p.t_sb + lb)
-                                  : load_index<int32_t>(p.tables, b * p.t_sb + lb);
-    if (e >= 0 && e < p.num_blocks) phys = (int)e;
-  }
-  return phys;
-}
 
 template <typename Tag, int D, int G>
 __global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParams p) {
@@ -141,7 +80,6 @@ __global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParam
   constexpr int TPT = C::TPT, CPL = C::CPL, LD = C::LD, ROWS = C::ROWS, R = C::R, TI = C::TI;
   constexpr int VEC = C::VEC, EB = C::EB;
   constexpr bool F32 = (EB == 4);
-  constexpr int QW = F32 ? 4 : 4;  // 32-bit words per chunk
 
   const int lane = threadIdx.x;
   const int row = lane / TPT;
@@ -157,9 +95,9 @@ __global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParam
   const int64_t part_end = ctx < part_start + p.partition_size ? ctx : part_start + p.partition_size;
   const int n_tiles = part_end > part_start ? (int)((part_end - part_start + TI - 1) / TI) : 0;
 
-  // ---- query heads of this group
-  const int head0 = qg * p.group_size;  // index inside the kv head's heads
-  uint32_t qw[G][CPL][QW];
+  // ---- query heads of this group, kept packed (two halves per word)
+  const int head0 = qg * p.group_size;  // index among the kv head's query heads
+  uint32_t qw[G][CPL][4];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const bool hv = (g < p.group_size) && (head0 + g < p.heads_per_kv);
@@ -186,50 +124,43 @@ __global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParam
 
   const char *kbase = p.kc + (int64_t)kvh * p.k_sh * EB;
   const char *vbase = p.vc + (int64_t)kvh * p.v_sh * EB;
+  const char *zero_row = reinterpret_cast<const char *>(g_zero_row);
   const int bs = p.block_size;
+  const int lane_off = sub * 16;
 
-  // Block-table window: lane j holds table[b, win_base + j].
-  int64_t win_base = -1000000;
-  int win = -1;
+  // Block-table window: lane j holds table[b, win_base + j] (or -1).
+  int64_t win_base = p.bs_shift >= 0 ? (part_start >> p.bs_shift) : part_start / bs;
+  int win = load_table_window(p, b, win_base, lane);
 
-  // Resolves the physical block of every row-step token of tile `t` and
-  // issues its K/V loads.
-  auto load_tile = [&](int t, u32x4 (&kr)[R][CPL], u32x4 (&vr)[R][CPL], uint32_t &valid) {
+  // Issues the K/V loads of tile `t` (unconditionally: masked lanes read
+  // the zero row) and returns the lane's valid-token mask.
+  auto issue_tile = [&](int t, u32x4 (&kr)[R][CPL], u32x4 (&vr)[R][CPL]) -> uint32_t {
     const int64_t tile_base = part_start + (int64_t)t * TI;
-    const int64_t lb_lo = p.bs_shift >= 0 ? (tile_base >> p.bs_shift) : tile_base / bs;
     const int64_t last = tile_base + TI - 1;
     const int64_t lb_hi = p.bs_shift >= 0 ? (last >> p.bs_shift) : last / bs;
-    if (lb_lo < win_base || lb_hi >= win_base + 64) {
-      win_base = lb_lo;
+    if (lb_hi >= win_base + 64) {  // wave-uniform: move the window forward
+      win_base = p.bs_shift >= 0 ? (tile_base >> p.bs_shift) : tile_base / bs;
       win = load_table_window(p, b, win_base, lane);
     }
-    valid = 0;
+    uint32_t valid = 0;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int64_t pos = tile_base + r * ROWS + row;
       const int64_t lb = p.bs_shift >= 0 ? (pos >> p.bs_shift) : pos / bs;
-      const int64_t off = pos - lb * bs;
-      const int64_t idx = lb - win_base;
-      int phys = __builtin_amdgcn_ds_bpermute((int)(idx & 63) * 4, win);
-      if (idx >= 64) phys = load_table_window(p, b, lb, 0);  // tile wider than the window
+      const int off = (int)(pos - lb * bs);
+      const int idx = (int)(lb - win_base);  // 0..63 by construction of the window
+      const int phys = __builtin_amdgcn_ds_bpermute((idx & 63) * 4, win);
       const bool ok = (pos < part_end) && (phys >= 0);
       valid |= (ok ? 1u : 0u) << r;
-      if (ok) {
-        const char *kr_row = kbase + ((int64_t)phys * p.k_sb + off * p.k_st) * EB;
-        const char *vr_row = vbase + ((int64_t)phys * p.v_sb + off * p.v_st) * EB;
+      const char *krow = ok ? kbase + ((int64_t)phys * p.k_sb + (int64_t)off * p.k_st) * EB : zero_row;
+      const char *vrow = ok ? vbase + ((int64_t)phys * p.v_sb + (int64_t)off * p.v_st) * EB : zero_row;
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          kr[r][c] = load16(kr_row + (c * TPT + sub) * 16);
-          vr[r][c] = load16(vr_row + (c * TPT + sub) * 16);
-        }
-      } else {
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          kr[r][c] = u32x4{0u, 0u, 0u, 0u};
-          vr[r][c] = u32x4{0u, 0u, 0u, 0u};
-        }
+      for (int c = 0; c < CPL; ++c) {
+        kr[r][c] = load16_stream(krow + c * TPT * 16 + lane_off);
+        vr[r][c] = load16_stream(vrow + c * TPT * 16 + lane_off);
       }
     }
+    return valid;
   };
 
   auto compute_tile = [&](const u32x4 (&kr)[R][CPL], const u32x4 (&vr)[R][CPL], uint32_t valid) {
@@ -255,7 +186,8 @@ __global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParam
         s[r][g] = ((valid >> r) & 1u) ? d : -INFINITY;
       }
     }
-    // Lazy online-softmax rescale.
+    // Lazy online-softmax rescale: only when a row's max grows by more
+    // than RESCALE_LOG2 (results are unchanged; weights stay <= 2^8).
     bool need_any = false;
     float tmax[G];
 #pragma unroll
@@ -308,18 +240,17 @@ __global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParam
     }
   };
 
-  // ---- software-pipelined tile loop: loads of tile t+1 fly while tile t computes
+  // ---- software pipeline, two register buffers: the loads of the next
+  // tile are in flight while the current one computes. Loads past the last
+  // tile are fully masked (zero row) so the issue pattern is straight-line.
   u32x4 ka[R][CPL], va[R][CPL], kb[R][CPL], vb[R][CPL];
-  uint32_t valid_a = 0, valid_b = 0;
-  if (n_tiles > 0) load_tile(0, ka, va, valid_a);
-  int t = 0;
-  for (; t + 1 < n_tiles; t += 2) {
-    load_tile(t + 1, kb, vb, valid_b);
+  uint32_t valid_a = issue_tile(0, ka, va);
+  for (int t = 0; t < n_tiles; t += 2) {
+    const uint32_t valid_b = issue_tile(t + 1, kb, vb);
     compute_tile(ka, va, valid_a);
-    if (t + 2 < n_tiles) load_tile(t + 2, ka, va, valid_a);
-    compute_tile(kb, vb, valid_b);
+    valid_a = issue_tile(t + 2, ka, va);
+    if (t + 1 < n_tiles) compute_tile(kb, vb, valid_b);
   }
-  if (t < n_tiles) compute_tile(ka, va, valid_a);
 
   // ---- merge the token rows of the wave (same sub, different row)
 #pragma unroll
@@ -349,7 +280,7 @@ __global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParam
     const int64_t hq = (int64_t)kvh * p.heads_per_kv + head0 + g;
     if (p.split) {
       const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;
-      const int64_t prow = (b * p.num_heads + hq) * p.num_parts + part;
+      const int64_t prow = (b * p.num_parts + part) * p.num_heads + hq;
       float *po = p.part_o + prow * D;
 #pragma unroll
       for (int c = 0; c < CPL; ++c) {
@@ -380,49 +311,71 @@ __global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParam
 
 // Combines the split partials of one (request, head):
 //   out = sum_p 2^(lse_p - M) o_p / sum_p 2^(lse_p - M),  M = max_p lse_p.
+// Lanes split into GROUPS groups of D/4 lanes; group j takes partitions
+// j, j+GROUPS, ... with 16-byte loads, so the loads of all partitions are in
+// flight together; the groups then combine through LDS.
 template <typename Tag, int D>
 __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(const AttnParams p) {
   constexpr int EB = elem<Tag>::bytes;
+  constexpr int CH = D / 4;           // float4 chunks per row
+  constexpr int GROUPS = 64 / CH;     // partition groups
+  __shared__ float4 part_sum[GROUPS][CH];
+  __shared__ float part_z[GROUPS];
   const int lane = threadIdx.x;
   const int64_t hq = blockIdx.x;
   const int64_t b = blockIdx.y;
   const int64_t ctx = p.lens_i64 ? load_index<int64_t>(p.lens, b) : load_index<int32_t>(p.lens, b);
   int np = ctx > 0 ? (int)((ctx + p.partition_size - 1) / p.partition_size) : 0;
   if (np > p.num_parts) np = p.num_parts;
-  const int64_t prow = (b * p.num_heads + hq) * p.num_parts;
+  // partial rows of this (request, head): (b * NP + i) * H + hq
+  const int64_t prow = b * p.num_parts * p.num_heads + hq;
+  const int64_t pstride = p.num_heads;
   float mx = -INFINITY;
-  for (int i = lane; i < np; i += 64) mx = fmaxf(mx, p.part_lse[prow + i]);
+  for (int i = lane; i < np; i += 64) mx = fmaxf(mx, p.part_lse[prow + i * pstride]);
 #pragma unroll
   for (int mask = 1; mask < 64; mask <<= 1) mx = fmaxf(mx, shfl_xor_f(mx, mask));
-  constexpr int PER = (D + 63) / 64;
-  float accv[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) accv[j] = 0.f;
+  const int grp = lane / CH;
+  const int ch = lane % CH;
+  float4 a = {0.f, 0.f, 0.f, 0.f};
   float z = 0.f;
-  for (int i = 0; i < np; ++i) {
-    const float w = fast_exp2(p.part_lse[prow + i] - mx);
-    z += w;
-    const float *po = p.part_o + (prow + i) * D;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int d = lane + 64 * j;
-      if (d < D) accv[j] = fmaf(w, po[d], accv[j]);
+  if (grp < GROUPS) {
+#pragma unroll 4
+    for (int i = grp; i < np; i += GROUPS) {
+      const float w = fast_exp2(p.part_lse[prow + i * pstride] - mx);
+      const float4 o = reinterpret_cast<const float4 *>(p.part_o + (prow + i * pstride) * D)[ch];
+      z += w;
+      a.x = fmaf(w, o.x, a.x);
+      a.y = fmaf(w, o.y, a.y);
+      a.z = fmaf(w, o.z, a.z);
+      a.w = fmaf(w, o.w, a.w);
     }
+    part_sum[grp][ch] = a;
+    if (ch == 0) part_z[grp] = z;
   }
-  const float inv = 1.f / z;
-  char *dst = p.out + (b * p.o_sb + hq * p.o_sh) * EB;
+  __syncthreads();
+  if (lane >= CH) return;
+  float4 t = part_sum[0][lane];
+  float zt = part_z[0];
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int d = lane + 64 * j;
-    if (d >= D) continue;
-    const float v = accv[j] * inv;
-    if constexpr (EB == 4) {
-      reinterpret_cast<float *>(dst)[d] = v;
-    } else if constexpr (__is_same(Tag, bf16_tag)) {
-      reinterpret_cast<uint16_t *>(dst)[d] = (uint16_t)f32_to_bf16_bits(v);
-    } else {
-      reinterpret_cast<_Float16 *>(dst)[d] = (_Float16)v;
-    }
+  for (int j = 1; j < GROUPS; ++j) {
+    const float4 u = part_sum[j][lane];
+    t.x += u.x;
+    t.y += u.y;
+    t.z += u.z;
+    t.w += u.w;
+    zt += part_z[j];
+  }
+  const float inv = 1.f / zt;
+  const float v[4] = {t.x * inv, t.y * inv, t.z * inv, t.w * inv};
+  char *dst = p.out + (b * p.o_sb + hq * p.o_sh) * EB + (int64_t)lane * 4 * EB;
+  if constexpr (EB == 4) {
+    store16(dst, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                       __float_as_uint(v[3])});
+  } else {
+    uint2 w;
+    w.x = elem<Tag>::pack2(v[0], v[1]);
+    w.y = elem<Tag>::pack2(v[2], v[3]);
+    *reinterpret_cast<uint2 *>(dst) = w;
   }
 }
 
@@ -460,6 +413,18 @@ int next_pow2(int x) {
 }
 
 constexpr int SCALAR_MAX_GROUP = 8;
+constexpr int MFMA_MAX_GROUP = 16;
+
+// Kernel family of a launch shape: one query head per KV head -> the
+// one-head scalar kernel; fp16/bf16 with an MFMA-compatible head_dim and
+// block size -> matrix cores; everything else -> the grouped scalar kernel.
+int select_path(int dtype, int head_dim, int block_size, int heads_per_kv, int query_group_size) {
+  if (heads_per_kv == 1) return IKL_PATH_MHA_FALLBACK;
+  int gs = query_group_size <= 0 || query_group_size > heads_per_kv ? heads_per_kv : query_group_size;
+  if (gs > MFMA_MAX_GROUP) gs = MFMA_MAX_GROUP;
+  if (mfma_supported(dtype, head_dim, block_size, gs)) return IKL_PATH_MFMA_GROUPED;
+  return IKL_PATH_SCALAR_GROUPED;
+}
 
 int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
   if (!a) return fail(IKL_EINVAL, "attention: null argument struct");
@@ -481,14 +446,25 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
     return fail(IKL_EUNSUPPORTED, "head_dim " + std::to_string(a->head_dim) +
                                       " is not compiled (supported: 16, 32, 64, 96, 128)");
   if (a->batch > 65535) return fail(IKL_EINVAL, "batch exceeds the grid limit (65535)");
+  if (a->query_group_size < 0) return fail(IKL_EINVAL, "query_group_size must be non-negative");
   pl.heads_per_kv = a->num_heads / a->num_kv_heads;
-  pl.path = IKL_PATH_SCALAR_GROUPED;
-  if (a->path == IKL_PATH_MHA_FALLBACK || pl.heads_per_kv == 1) pl.path = IKL_PATH_MHA_FALLBACK;
-  int gs = a->query_group_size;
-  if (gs < 0) return fail(IKL_EINVAL, "query_group_size must be non-negative");
-  if (gs == 0 || gs > pl.heads_per_kv) gs = pl.heads_per_kv;
+  const int requested_gs = a->query_group_size;
+  if (a->path == -1) {
+    pl.path = select_path(a->dtype, a->head_dim, a->block_size, pl.heads_per_kv, requested_gs);
+  } else if (a->path == IKL_PATH_MHA_FALLBACK || a->path == IKL_PATH_SCALAR_GROUPED) {
+    pl.path = pl.heads_per_kv == 1 ? IKL_PATH_MHA_FALLBACK : a->path;
+  } else if (a->path == IKL_PATH_MFMA_GROUPED) {
+    pl.path = IKL_PATH_MFMA_GROUPED;
+  } else {
+    return fail(IKL_EINVAL, "attention: unknown kernel path");
+  }
+  int gs = requested_gs == 0 || requested_gs > pl.heads_per_kv ? pl.heads_per_kv : requested_gs;
   if (pl.path == IKL_PATH_MHA_FALLBACK) gs = 1;
-  if (gs > SCALAR_MAX_GROUP) gs = SCALAR_MAX_GROUP;
+  const int cap_gs = pl.path == IKL_PATH_MFMA_GROUPED ? MFMA_MAX_GROUP : SCALAR_MAX_GROUP;
+  if (gs > cap_gs) gs = cap_gs;
+  if (pl.path == IKL_PATH_MFMA_GROUPED && !mfma_supported(a->dtype, a->head_dim, a->block_size, gs))
+    return fail(IKL_EUNSUPPORTED,
+                "MFMA path needs fp16/bf16, head_dim 32/64/96/128 and a block size multiple of 16");
   pl.group_size = gs;
   pl.gmax = next_pow2(gs);
   pl.groups_per_kv = (pl.heads_per_kv + gs - 1) / gs;
@@ -533,33 +509,44 @@ void record(void *ev, hipStream_t s) {
 }
 
 template <typename Tag, int D>
-hipError_t launch_scalar(const Plan &pl, const AttnParams &p, dim3 grid, hipStream_t s,
-                         void *const *events) {
-  record(events[0], s);
-  switch (pl.gmax) {
+void launch_scalar(int gmax, const AttnParams &p, dim3 grid, hipStream_t s) {
+  switch (gmax) {
     case 1: paged_decode_scalar_kernel<Tag, D, 1><<<grid, 64, 0, s>>>(p); break;
     case 2: paged_decode_scalar_kernel<Tag, D, 2><<<grid, 64, 0, s>>>(p); break;
     case 4: paged_decode_scalar_kernel<Tag, D, 4><<<grid, 64, 0, s>>>(p); break;
     default: paged_decode_scalar_kernel<Tag, D, 8><<<grid, 64, 0, s>>>(p); break;
   }
-  record(events[1], s);
-  if (pl.split) {
-    dim3 rgrid((unsigned)p.num_heads, grid.z);
-    paged_decode_reduce_kernel<Tag, D><<<rgrid, 64, 0, s>>>(p);
-  }
-  record(events[2], s);
-  return hipGetLastError();
+}
+
+template <typename Tag, int D>
+void launch_reduce(const AttnParams &p, dim3 grid, hipStream_t s) {
+  dim3 rgrid((unsigned)p.num_heads, grid.z);
+  paged_decode_reduce_kernel<Tag, D><<<rgrid, 64, 0, s>>>(p);
 }
 
 template <typename Tag>
-hipError_t launch_dim(int d, const Plan &pl, const AttnParams &p, dim3 grid, hipStream_t s,
-                      void *const *ev) {
+void launch_family(int d, const Plan &pl, const AttnParams &p, dim3 grid, hipStream_t s, int dtype) {
+  if (pl.path == IKL_PATH_MFMA_GROUPED) {
+    (void)launch_mfma_attention(dtype, d, p, grid, s);
+    return;
+  }
   switch (d) {
-    case 16: return launch_scalar<Tag, 16>(pl, p, grid, s, ev);
-    case 32: return launch_scalar<Tag, 32>(pl, p, grid, s, ev);
-    case 64: return launch_scalar<Tag, 64>(pl, p, grid, s, ev);
-    case 96: return launch_scalar<Tag, 96>(pl, p, grid, s, ev);
-    default: return launch_scalar<Tag, 128>(pl, p, grid, s, ev);
+    case 16: launch_scalar<Tag, 16>(pl.gmax, p, grid, s); break;
+    case 32: launch_scalar<Tag, 32>(pl.gmax, p, grid, s); break;
+    case 64: launch_scalar<Tag, 64>(pl.gmax, p, grid, s); break;
+    case 96: launch_scalar<Tag, 96>(pl.gmax, p, grid, s); break;
+    default: launch_scalar<Tag, 128>(pl.gmax, p, grid, s); break;
+  }
+}
+
+template <typename Tag>
+void launch_reduce_dim(int d, const AttnParams &p, dim3 grid, hipStream_t s) {
+  switch (d) {
+    case 16: launch_reduce<Tag, 16>(p, grid, s); break;
+    case 32: launch_reduce<Tag, 32>(p, grid, s); break;
+    case 64: launch_reduce<Tag, 64>(p, grid, s); break;
+    case 96: launch_reduce<Tag, 96>(p, grid, s); break;
+    default: launch_reduce<Tag, 128>(p, grid, s); break;
   }
 }
 
@@ -584,14 +571,11 @@ extern "C" int32_t ikl_paged_attention_partition_size(const ikl_paged_attention_
   return pl.split ? pl.partition : 0;
 }
 
-extern "C" int32_t ikl_paged_attention_path(int32_t dtype, int32_t head_dim, int64_t table_width,
-                                            int32_t heads_per_kv, int32_t query_group_size) {
-  (void)dtype;
-  (void)head_dim;
+extern "C" int32_t ikl_paged_attention_path(int32_t dtype, int32_t head_dim, int32_t block_size,
+                                            int64_t table_width, int32_t heads_per_kv,
+                                            int32_t query_group_size) {
   (void)table_width;
-  (void)query_group_size;
-  if (heads_per_kv == 1) return IKL_PATH_MHA_FALLBACK;
-  return IKL_PATH_SCALAR_GROUPED;
+  return select_path(dtype, head_dim, block_size, heads_per_kv, query_group_size);
 }
 
 extern "C" int ikl_paged_attention(const ikl_paged_attention_args *a, void *stream) {
@@ -651,12 +635,22 @@ extern "C" int ikl_paged_attention(const ikl_paged_attention_args *a, void *stre
 
   dim3 grid((unsigned)pl.num_parts, (unsigned)(a->num_kv_heads * pl.groups_per_kv), (unsigned)a->batch);
   hipStream_t s = (hipStream_t)stream;
-  hipError_t e;
+  record(a->events[0], s);
   switch (a->dtype) {
-    case IKL_F16: e = launch_dim<f16_tag>(a->head_dim, pl, p, grid, s, a->events); break;
-    case IKL_BF16: e = launch_dim<bf16_tag>(a->head_dim, pl, p, grid, s, a->events); break;
-    default: e = launch_dim<f32_tag>(a->head_dim, pl, p, grid, s, a->events); break;
+    case IKL_F16: launch_family<f16_tag>(a->head_dim, pl, p, grid, s, a->dtype); break;
+    case IKL_BF16: launch_family<bf16_tag>(a->head_dim, pl, p, grid, s, a->dtype); break;
+    default: launch_family<f32_tag>(a->head_dim, pl, p, grid, s, a->dtype); break;
   }
+  record(a->events[1], s);
+  if (pl.split) {
+    switch (a->dtype) {
+      case IKL_F16: launch_reduce_dim<f16_tag>(a->head_dim, p, grid, s); break;
+      case IKL_BF16: launch_reduce_dim<bf16_tag>(a->head_dim, p, grid, s); break;
+      default: launch_reduce_dim<f32_tag>(a->head_dim, p, grid, s); break;
+    }
+  }
+  record(a->events[2], s);
+  const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(IKL_ELAUNCH, std::string("paged attention launch: ") + hipGetErrorString(e));
   return IKL_OK;
 }

@@ -67,16 +67,28 @@ def paged_decode_grouped_path(
     table_width: int,
     heads_per_kv: int,
     query_group_size: int,
+    block_size: int = 16,
 ) -> str:
     """Kernel family a grouped launch of this static shape runs.
 
-    ``"mha_fallback"`` when every KV head serves one query head, else
+    ``"mha_fallback"`` when every KV head serves one query head;
+    ``"mfma_grouped"`` (matrix cores) for fp16/bf16 caches with head_dim in
+    {32, 64, 96, 128} and a block size that is a multiple of 16; otherwise
     ``"scalar_grouped"`` (the query group shares each K/V tile on the VALU).
-    Pure function of its arguments, like triton_ops.py:56-75; the library's
-    ``ikl_paged_attention_path`` applies the same rule.
+    Pure function of its arguments, like triton_ops.py:56-75; ``block_size``
+    (keyword, default 16 like the reference's caches) is an addition the
+    MFMA tiles need. The library's ``ikl_paged_attention_path`` applies the
+    same rule.
     """
     if heads_per_kv == 1:
         return "mha_fallback"
+    if (
+        dtype in (torch.float16, torch.bfloat16)
+        and head_dim in (32, 64, 96, 128)
+        and block_size > 0
+        and block_size % 16 == 0
+    ):
+        return "mfma_grouped"
     return "scalar_grouped"
 
 
@@ -316,6 +328,7 @@ def paged_decode_attention_hip_grouped(
         table_width=block_tables.shape[1],
         heads_per_kv=heads_per_kv,
         query_group_size=query_group_size,
+        block_size=cache.layout.block_size,
     )
     return _launch_attention(
         query,

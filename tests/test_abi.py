@@ -88,22 +88,31 @@ def test_invalid_arguments_report_errors():
 
 
 @pytest.mark.parametrize(
-    ("dtype", "table_width", "heads_per_kv", "expected"),
+    ("dtype", "head_dim", "block_size", "table_width", "heads_per_kv", "expected"),
     [
-        (torch.float16, 8, 4, "scalar_grouped"),
-        (torch.bfloat16, 16, 32, "scalar_grouped"),
-        (torch.float16, 17, 32, "scalar_grouped"),
-        (torch.float32, 8, 32, "scalar_grouped"),
-        (torch.float16, 8, 1, "mha_fallback"),
+        # the cases of tests/test_attention.py:22-42 (head_dim 64, block 16)
+        (torch.float16, 64, 16, 8, 4, "mfma_grouped"),
+        (torch.bfloat16, 64, 16, 16, 32, "mfma_grouped"),
+        (torch.float16, 64, 16, 17, 32, "mfma_grouped"),
+        (torch.float32, 64, 16, 8, 32, "scalar_grouped"),
+        (torch.float16, 64, 16, 8, 1, "mha_fallback"),
+        # shapes the MFMA tiles cannot take
+        (torch.bfloat16, 16, 16, 8, 4, "scalar_grouped"),
+        (torch.bfloat16, 128, 8, 8, 4, "scalar_grouped"),
+        (torch.bfloat16, 128, 32, 8, 4, "mfma_grouped"),
+        (torch.float16, 80, 16, 8, 4, "scalar_grouped"),
     ],
 )
-def test_grouped_path_truth_table_matches_library(dtype, table_width, heads_per_kv, expected):
-    """Same cases as tests/test_attention.py:22-42, answered with this
+def test_grouped_path_truth_table_matches_library(dtype, head_dim, block_size, table_width,
+                                                  heads_per_kv, expected):
+    """Same role as tests/test_attention.py:22-42, answered with this
     library's families; the Python selector and the C one agree."""
-    got = ops.paged_decode_grouped_path(dtype=dtype, head_dim=64, table_width=table_width,
-                                        heads_per_kv=heads_per_kv, query_group_size=8)
+    got = ops.paged_decode_grouped_path(dtype=dtype, head_dim=head_dim, table_width=table_width,
+                                        heads_per_kv=heads_per_kv, query_group_size=8,
+                                        block_size=block_size)
     assert got == expected
-    code = _lib.load().ikl_paged_attention_path(ops._DTYPES[dtype], 64, table_width, heads_per_kv, 8)
+    code = _lib.load().ikl_paged_attention_path(ops._DTYPES[dtype], head_dim, block_size, table_width,
+                                                heads_per_kv, 8)
     assert ops._PATH_NAMES[code] == expected
 
 
