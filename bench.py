@@ -8,8 +8,11 @@ order of the reference's decode step (decode.py:480-487).
 Default workload (the GQA decode shape): batch 32, 32 query heads / 8 KV
 heads, head_dim 128, bf16, block size 16, ragged context lengths uniform in
 [4096, 8192] (seeded), block tables drawn by random permutation from a pool
-of 20,000 physical blocks, K/V/q ~ N(0,1), 512-token partitions. Inputs are
-resident in HBM before the timed region.
+of 20,000 physical blocks, K/V/q ~ N(0,1). The split is the library's
+automatic choice (on the MFMA family: the balanced split, one equal run of
+tiles per resident wave, merged by the reduce kernel); ``--partition-size
+512`` selects fixed 512-token partitions instead. Inputs are resident in HBM
+before the timed region.
 
 Prints ONE JSON line. ``value`` is the algorithmic HBM bytes of a step
 divided by its wall time (GB/s); ``roofline`` times the attention partition
@@ -37,7 +40,7 @@ METRIC = "paged decode attn µs/step + HBM GB/s (% peak), GQA 32/8 hd128 bf16"
 
 WORKLOADS = {
     # name: (batch, heads, kv_heads, head_dim, dtype, ctx_lo, ctx_hi, pool, kv_scale, partition)
-    "gqa32x8_hd128_bf16_b32_ctx4k-8k": (32, 32, 8, 128, torch.bfloat16, 4096, 8192, 20000, 1.0, 512),
+    "gqa32x8_hd128_bf16_b32_ctx4k-8k": (32, 32, 8, 128, torch.bfloat16, 4096, 8192, 20000, 1.0, None),
     "mha32_hd128_fp16_b16_ctx512": (16, 32, 32, 128, torch.float16, 512, 512, None, 1.0, None),
     "mqa32x1_hd128_bf16_b64_ctx1k-4k": (64, 32, 1, 128, torch.bfloat16, 1024, 4096, None, 0.5, None),
 }
@@ -137,8 +140,9 @@ def step_bytes(w) -> tuple[int, int]:
 
 
 def cpu_baseline(w, budget_s: float) -> dict:
-    """Times the CPU oracle (numpy paged_reference) on the first requests of
-    the same workload until ~budget_s of CPU work, then scales to one step."""
+    """Times the CPU oracle (numpy paged_reference) on the requests of the
+    same workload, cycling through the batch until ~budget_s of CPU work,
+    then scales the mean per-request time to one step."""
     import numpy as np
     from oracle import paged_oracle as po
 
@@ -160,25 +164,28 @@ def cpu_baseline(w, budget_s: float) -> dict:
 
     oc.k, oc.v = host(cache.k), host(cache.v)
     q = po.to_f32(host(w["query"]), dtype)
-    done, elapsed, kv_bytes = 0, 0.0, 0
+    done, elapsed, kv_bytes, ctx_tokens = 0, 0.0, 0, 0
     eb = cache.k.element_size()
-    while done < len(w["lengths"]) and elapsed < budget_s:
-        b = done
+    batch = len(w["lengths"])
+    while elapsed < budget_s:
+        b = done % batch
         t0 = time.perf_counter()
         po.paged_decode_attention(q[b : b + 1], oc, [w["tables_list"][b]], [w["lengths"][b]])
         elapsed += time.perf_counter() - t0
         kv_bytes += w["lengths"][b] * w["kv_heads"] * w["head_dim"] * 2 * eb
+        ctx_tokens += w["lengths"][b]
         done += 1
-    per_request_s = elapsed / done
-    step_s = per_request_s * len(w["lengths"])
+    # per-token cost scaled to the step's context tokens
+    step_s = elapsed / ctx_tokens * sum(w["lengths"])
     return {
         "value": round(step_s * 1e6, 1),
         "unit": "us/step",
         "gbps": round(kv_bytes / elapsed / 1e9, 3),
         "cores": threads,
         "kind": "port",
-        "sample": f"oracle paged_reference (numpy fp32) on the first {done} of {len(w['lengths'])} "
-                  f"requests ({elapsed:.1f} s), scaled to the full batch",
+        "sample": f"oracle paged_reference (numpy fp32), {done} single-request attentions cycling "
+                  f"through the {batch} requests ({ctx_tokens} context tokens, {elapsed:.1f} s), "
+                  f"scaled per context token to the full step",
     }
 
 
@@ -188,7 +195,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
-    parser.add_argument("--partition-size", type=int, default=None)
+    parser.add_argument("--partition-size", type=int, default=None,
+                        help="tokens per fixed split partition (default: the library's automatic split)")
     parser.add_argument("--cpu-budget-s", type=float, default=15.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--seed", type=int, default=0)
@@ -278,7 +286,9 @@ def main() -> int:
             "num_blocks": w["pool"],
             "context_tokens": sum(w["lengths"]),
             "partition_size": attn.partition_size,
-            "step": "paged attention (partition + reduce) then 1-token KV append per request",
+            "split": "balanced (equal tile runs per resident wave)" if attn.balanced_split
+                     else f"fixed partitions of {attn.partition_size} tokens",
+            "step": "paged attention (split kernel + reduce) then 1-token KV append per request",
             "parallelism": "single GPU",
         },
         "attention_kernel_us": round(kern_avg_ms * 1e3, 2),
@@ -291,7 +301,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
-            "kernel": "paged_decode_scalar_kernel",
+            "kernel": attn.kernel_names()[0],
             "algorithmic_bytes_per_launch": attn_bytes,
         },
         "cpu_baseline": cpu,

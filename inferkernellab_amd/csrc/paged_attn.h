@@ -42,6 +42,17 @@ struct AttnParams {
   int32_t table_i64;
   int32_t lens_i64;
   float scale_log2;        // scale * log2(e)
+  // Balanced ("stream-K") split of the MFMA family; sk_waves == 0 selects
+  // the fixed partitions above. With sk_waves = W, the global sequence of
+  // 16-token tiles — request-major, then (kv head, query group) unit, then
+  // position — is cut into W equal runs, one per wave; the piece of unit s
+  // (= b * units + u) that wave w covers lands in partial slot s + w (the
+  // pairs (s, w) met along the sequence are ordered in both s and w, so the
+  // slots are distinct and each unit's pieces are consecutive).
+  int32_t sk_waves;
+  int32_t units;           // kv heads x query groups per request
+  int64_t batch;
+  int64_t cap_tokens;      // table_width * block_size: positions a table can map
 };
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -96,10 +107,61 @@ __device__ inline int load_table_window(const AttnParams &p, int64_t b, int64_t 
   return phys;
 }
 
+// ---------------------------------------------------- balanced split helpers
+// Context length clamped to [0, cap_tokens] (positions past the table are
+// masked anyway, so they are not scheduled).
+__device__ inline int64_t clamped_ctx(const AttnParams &p, int64_t b) {
+  int64_t c = p.lens_i64 ? load_index<int64_t>(p.lens, b) : load_index<int32_t>(p.lens, b);
+  c = c < 0 ? 0 : c;
+  return c < p.cap_tokens ? c : p.cap_tokens;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ inline int wave_incl_scan(int x, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  return x;
+}
+
+// Request-level tile totals of the balanced split: tiles of all requests
+// before b (*before), of b itself (*own) and of the whole batch (return),
+// in request-tile units (multiply by p.units for global tiles). The host
+// bounds cap_tokens so that a 64-request chunk sum fits in 32 bits.
+__device__ inline int64_t request_tiles(const AttnParams &p, int64_t b, int lane, int64_t *before,
+                                        int *own) {
+  int64_t base = 0, total = 0;
+  *before = 0;
+  *own = 0;
+  for (int64_t c0 = 0; c0 < p.batch; c0 += 64) {
+    const int64_t r = c0 + lane;
+    const int n = r < p.batch ? (int)((clamped_ctx(p, r) + 15) >> 4) : 0;
+    const int incl = wave_incl_scan(n, lane);
+    if (b >= c0 && b < c0 + 64) {
+      const int l = (int)(b - c0);
+      *own = __shfl(n, l, 64);
+      *before = base + __shfl(incl, l, 64) - *own;
+    }
+    base += __shfl(incl, 63, 64);
+  }
+  total = base;
+  return total;
+}
+
+// The wave of a balanced split over T tiles and W waves (W <= T) whose run
+// [floor(w T / W), floor((w + 1) T / W)) holds global tile g.
+__device__ inline int64_t wave_of_tile(int64_t g, int64_t T, int64_t W) { return ((g + 1) * W - 1) / T; }
+
 // MFMA kernel family (paged_decode_mfma.hip). mfma_supported() tells whether
 // a (dtype, head_dim, block_size, group) launch has a compiled MFMA kernel;
-// launch_mfma_attention() enqueues it (grid as for the scalar family).
+// launch_mfma_attention() enqueues it (grid as for the scalar family, or
+// p.sk_waves one-wave workgroups for the balanced split).
 bool mfma_supported(int dtype, int head_dim, int block_size, int group_size);
 hipError_t launch_mfma_attention(int dtype, int head_dim, const AttnParams &p, dim3 grid, hipStream_t s);
+// One-wave workgroups of the balanced-split MFMA kernel resident at once on
+// the current device (the split's wave count).
+int mfma_streamk_capacity(int dtype, int head_dim);
 
 }  // namespace ikl

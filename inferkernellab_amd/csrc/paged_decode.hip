@@ -324,12 +324,33 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(const AttnParam
   const int lane = threadIdx.x;
   const int64_t hq = blockIdx.x;
   const int64_t b = blockIdx.y;
-  const int64_t ctx = p.lens_i64 ? load_index<int64_t>(p.lens, b) : load_index<int32_t>(p.lens, b);
-  int np = ctx > 0 ? (int)((ctx + p.partition_size - 1) / p.partition_size) : 0;
-  if (np > p.num_parts) np = p.num_parts;
-  // partial rows of this (request, head): (b * NP + i) * H + hq
-  const int64_t prow = b * p.num_parts * p.num_heads + hq;
-  const int64_t pstride = p.num_heads;
+  int np;
+  int64_t prow, pstride;
+  if (p.sk_waves > 0) {
+    // balanced split: unit u's pieces sit in consecutive slots s + w for the
+    // waves w whose runs cover its tiles; rows slot * group_size + head.
+    int64_t before;
+    int own;
+    const int64_t total = request_tiles(p, b, lane, &before, &own);
+    const int64_t U = p.units;
+    const int64_t T = U * total;
+    const int64_t W = (int64_t)p.sk_waves < T ? (int64_t)p.sk_waves : T;
+    const int kvh = (int)(hq / p.heads_per_kv), r = (int)(hq % p.heads_per_kv);
+    const int64_t u = (int64_t)kvh * p.groups_per_kv + r / p.group_size;
+    const int64_t s = U * before + u * own;  // first global tile of the unit
+    const int64_t w_lo = own > 0 ? wave_of_tile(s, T, W) : 0;
+    const int64_t w_hi = own > 0 ? wave_of_tile(s + own - 1, T, W) : -1;
+    np = (int)(w_hi - w_lo + 1);
+    prow = (b * U + u + w_lo) * p.group_size + r % p.group_size;
+    pstride = p.group_size;
+  } else {
+    const int64_t ctx = p.lens_i64 ? load_index<int64_t>(p.lens, b) : load_index<int32_t>(p.lens, b);
+    np = ctx > 0 ? (int)((ctx + p.partition_size - 1) / p.partition_size) : 0;
+    if (np > p.num_parts) np = p.num_parts;
+    // partial rows of this (request, head): (b * NP + i) * H + hq
+    prow = b * p.num_parts * p.num_heads + hq;
+    pstride = p.num_heads;
+  }
   float mx = -INFINITY;
   for (int i = lane; i < np; i += 64) mx = fmaxf(mx, p.part_lse[prow + i * pstride]);
 #pragma unroll
@@ -391,6 +412,8 @@ struct Plan {
   int partition = 0;  // tokens per grid.x slot
   int num_parts = 1;
   bool split = false;
+  int sk_waves = 0;  // balanced split (MFMA family): waves sharing the batch's tiles
+  int64_t units = 0;  // kv heads x query groups per request
   int64_t ws_o_bytes = 0;
   int64_t ws_bytes = 0;
 };
@@ -472,7 +495,27 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
   // Split-context partitions.
   const int64_t cap = a->table_width * (int64_t)a->block_size;
   int64_t maxctx = a->max_context_len > 0 ? std::min<int64_t>(a->max_context_len, cap) : cap;
-  const int64_t units = a->batch * (int64_t)a->num_kv_heads * pl.groups_per_kv;
+  pl.units = (int64_t)a->num_kv_heads * pl.groups_per_kv;
+  const int64_t units = a->batch * pl.units;
+
+  // Automatic split on the MFMA family: the balanced split (one run of
+  // ~T/W tiles per resident wave). Its in-kernel sums need a 64-request
+  // chunk of tile counts to fit in 32 bits (cap < 2^29 tokens) and
+  // (T + 1) * W to fit in 63 bits.
+  if (a->partition_size == 0 && pl.path == IKL_PATH_MFMA_GROUPED && cap < (int64_t(1) << 29)) {
+    const int64_t t_max = units * ((maxctx + 15) / 16);
+    const int64_t w = std::min<int64_t>(mfma_streamk_capacity(a->dtype, a->head_dim), std::max<int64_t>(t_max, 1));
+    if ((double)(t_max + 1) * (double)w < 4.0e18) {
+      pl.sk_waves = (int)w;
+      pl.split = true;
+      pl.num_parts = 1;
+      pl.partition = (int)std::min<int64_t>(16 * ((t_max + w - 1) / w), 0x7fffffffLL);
+      const int64_t rows = (units + w) * pl.group_size;
+      pl.ws_o_bytes = ((rows * a->head_dim * 4) + 255) / 256 * 256;
+      pl.ws_bytes = pl.ws_o_bytes + rows * 4;
+      return IKL_OK;
+    }
+  }
   int64_t P;
   if (a->partition_size == -1) {
     P = maxctx;
@@ -632,6 +675,10 @@ extern "C" int ikl_paged_attention(const ikl_paged_attention_args *a, void *stre
   p.table_i64 = a->table_type == IKL_I64;
   p.lens_i64 = a->lens_type == IKL_I64;
   p.scale_log2 = a->scale * LOG2E;
+  p.sk_waves = pl.sk_waves;
+  p.units = (int32_t)pl.units;
+  p.batch = a->batch;
+  p.cap_tokens = a->table_width * (int64_t)a->block_size;
 
   dim3 grid((unsigned)pl.num_parts, (unsigned)(a->num_kv_heads * pl.groups_per_kv), (unsigned)a->batch);
   hipStream_t s = (hipStream_t)stream;

@@ -2,9 +2,9 @@
 //
 // Same result as the scalar family (paged_reference, attention.py:134-175);
 // used for fp16/bf16 caches with head_dim in {32, 64, 96, 128} and a block
-// size that is a multiple of 16. One wave per (partition, kv head, query
-// group of <= 16 heads, request) walks its partition in 16-token tiles (a
-// tile never crosses a block, so it needs one block-table entry):
+// size that is a multiple of 16. A wave attends one (request, kv head,
+// query group of <= 16 heads) over a run of 16-token tiles (a tile never
+// crosses a block, so it needs one block-table entry):
 //
 //   S^T[16 tok x 16 heads] = K[16 x D] . Q^T      D/32 v_mfma_f32_16x16x32
 //   online softmax on S (lane = one head x 4 tokens; lazily rescaled)
@@ -16,6 +16,15 @@
 // row-major in LDS (16-byte pieces rotated by row to spread banks) and read
 // back transposed with ds_read_b64_tr_b16, which hands each lane four
 // consecutive tokens of one head_dim column: the V^T operand.
+//
+// Two schedules share that tile loop:
+//  * fixed partitions (paged_decode_mfma_kernel): a workgroup of WAVES
+//    waves per (partition, unit, request); its waves split the partition's
+//    tiles and merge their softmax states in LDS before one store;
+//  * balanced split (paged_decode_mfma_streamk_kernel): exactly as many
+//    one-wave workgroups as the GPU holds at once, each taking an equal run
+//    of the batch's global tile sequence (see AttnParams::sk_waves), so every
+//    wave starts once, streams ~T/W tiles and all finish together.
 //
 // MFMA operand layouts (gfx950; 16x16x32 checked by a lane-layout probe):
 //   16x16x32: lane l supplies A[l%16][8(l/16)+j], B[8(l/16)+j][l%16], j < 8;
@@ -43,6 +52,9 @@ constexpr int TILE = 16;  // tokens per tile
 
 // Tuning knobs: tiles prefetched ahead of the one computing (1 or 2), and an
 // optional minimum-occupancy request to the register allocator.
+#ifndef IKL_MFMA_HEAD_MAJOR
+#define IKL_MFMA_HEAD_MAJOR 1
+#endif
 #ifndef IKL_MFMA_PREFETCH
 #define IKL_MFMA_PREFETCH 1
 #endif
@@ -90,232 +102,428 @@ struct mfma_ops<f16_tag> {
 
 __device__ inline v4u32 zero4() { return v4u32{0u, 0u, 0u, 0u}; }
 
+// Per-wave state of the tile loop: lane constants, the Q^T operand and the
+// running softmax state (acc, m, lsum) of one (request, unit) run.
 template <typename Tag, int D>
-__global__ __launch_bounds__(64) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_kernel(const AttnParams p) {
+struct WaveTiles {
   static_assert(D % 32 == 0 && D <= 128, "MFMA path needs head_dim = 32k <= 128");
-  constexpr int EB = 2;
-  constexpr int KSTEPS = D / 32;              // QK^T k-steps
-  constexpr int MTILES = D / 16;              // PV output tiles of 16 dims
-  constexpr int PIECES = D * EB / 16;         // 16-byte pieces per row
-  constexpr int ROWB = D * EB;                // bytes per K/V row
-  constexpr int VLOADS = (TILE * PIECES + 63) / 64;  // 16-byte V loads per lane per tile
-  // V tile staging during the loop; the wave's [16 heads x D] fp32 results
-  // at the end (coalesced stores), hence the larger of the two sizes.
-  __shared__ __attribute__((aligned(16))) char vtile[16 * D * 4 > TILE * ROWB ? 16 * D * 4 : TILE * ROWB];
+  static constexpr int EB = 2;
+  static constexpr int KSTEPS = D / 32;                     // QK^T k-steps
+  static constexpr int MTILES = D / 16;                     // PV output tiles of 16 dims
+  static constexpr int PIECES = D * EB / 16;                // 16-byte pieces per row
+  static constexpr int ROWB = D * EB;                       // bytes per K/V row
+  static constexpr int VLOADS = (TILE * PIECES + 63) / 64;  // 16-byte V loads per lane per tile
+  static constexpr int VT_BYTES = TILE * ROWB;              // one staged V tile
+  static constexpr int SROW = D + 4;                        // staged fp32 row (padded vs bank conflicts)
+  static constexpr int ST_BYTES = 16 * SROW * 4;            // one staged [16 heads x D] block
   using ops = mfma_ops<Tag>;
 
-  const int lane = threadIdx.x;
-  const int hl = lane & 15;   // MFMA row/column index inside a 16-lane group
-  const int grp = lane >> 4;  // 16-lane group
+  struct Tile {
+    v4u32 k[KSTEPS];
+    v4u32 v[VLOADS];
+    int n_valid;  // tokens of the tile inside the run with a valid block (0..16)
+  };
+
+  int lane, hl, grp;
+  int k_lane;
+  int v_lds[VLOADS], v_lane[VLOADS], tr_lds[MTILES];
+  v4u32 qb[KSTEPS];
+  f32x4_t acc[MTILES];
+  float m, lsum;
+
+  __device__ __forceinline__ explicit WaveTiles(const AttnParams &p) {
+    lane = threadIdx.x & 63;
+    hl = lane & 15;   // MFMA row/column index inside a 16-lane group
+    grp = lane >> 4;  // 16-lane group
+    k_lane = (hl * (int)p.k_st + 8 * grp) * EB;  // token hl, dims 8g.. of each k-step
+#pragma unroll
+    for (int u = 0; u < VLOADS; ++u) {
+      const int pi = u * 64 + lane;  // V piece: row pi / PIECES, piece pi % PIECES
+      const int row = pi / PIECES < TILE ? pi / PIECES : TILE - 1, c = pi % PIECES;
+      v_lds[u] = row * ROWB + ((c + row) % PIECES) * 16;
+      v_lane[u] = row * (int)p.v_st * EB + c * 16;
+    }
+#pragma unroll
+    for (int mt = 0; mt < MTILES; ++mt) {  // V^T reads: token 4g + (l%16)/4, dims 16mt + 4((l%16)%4)
+      const int row = 4 * grp + (hl >> 2);
+      const int c = 2 * mt + ((hl & 3) >> 1);
+      tr_lds[mt] = row * ROWB + ((c + row) % PIECES) * 16 + (hl & 1) * 8;
+    }
+  }
+
+  // Q^T operand: lane l holds q[hq(l%16)][32s + 8(l/16) .. +7].
+  __device__ __forceinline__ void load_q(const AttnParams &p, int64_t b, int64_t hq, bool head_ok) {
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      qb[s] = zero4();
+      if (head_ok) qb[s] = load16v_global(p.q + (b * p.q_sb + hq * p.q_sh + 32 * s + 8 * grp) * EB);
+    }
+  }
+
+  // Attends positions [t0, t1) of request b against kv head kvh (t0 is a
+  // multiple of TILE) into fresh acc / m / lsum; lsum ends summed over the
+  // four lane groups. vtile: this wave's VT_BYTES of LDS.
+  __device__ __forceinline__ void attend(const AttnParams &p, int64_t b, int kvh, int64_t t0, int64_t t1,
+                                         char *vtile) {
+#pragma unroll
+    for (int mt = 0; mt < MTILES; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    m = NEG_SENTINEL;
+    lsum = 0.f;
+    const int n_tiles = t1 > t0 ? (int)((t1 - t0 + TILE - 1) / TILE) : 0;
+    const char *kbase = p.kc + (int64_t)kvh * p.k_sh * EB;
+    const char *vbase = p.vc + (int64_t)kvh * p.v_sh * EB;
+    const char *zero_row = reinterpret_cast<const char *>(g_zero_row);
+    const int bs = p.block_size;
+    int64_t win_base = p.bs_shift >= 0 ? (t0 >> p.bs_shift) : t0 / bs;
+    int win = load_table_window(p, b, win_base, lane);
+
+    // Resolves tile t's block and issues its K/V loads (straight-line:
+    // masked rows read the zero row).
+    auto issue = [&](int t, Tile &T) {
+      const int64_t base = t0 + (int64_t)t * TILE;
+      const int64_t lb = p.bs_shift >= 0 ? (base >> p.bs_shift) : base / bs;
+      if (lb >= win_base + 64) {
+        win_base = lb;
+        win = load_table_window(p, b, win_base, lane);
+      }
+      const int64_t off = base - lb * bs;
+      const int phys = __builtin_amdgcn_readlane(win, (int)(lb - win_base));
+      const int64_t left = t1 - base;
+      T.n_valid = phys < 0 || left <= 0 ? 0 : (left >= TILE ? TILE : (int)left);
+      const int64_t kro = ((int64_t)phys * p.k_sb + off * p.k_st) * EB;
+      const int64_t vro = ((int64_t)phys * p.v_sb + off * p.v_st) * EB;
+      const bool k_ok = hl < T.n_valid;
+      const char *kr = k_ok ? kbase + kro + k_lane : zero_row;
+      const int kstep = k_ok ? 64 : 0;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) T.k[s] = load16v_stream(kr + s * kstep);
+#pragma unroll
+      for (int u = 0; u < VLOADS; ++u) {
+        const int row = (u * 64 + lane) / PIECES;
+        const bool v_ok = row < T.n_valid;
+        T.v[u] = load16v_stream(v_ok ? vbase + vro + v_lane[u] : zero_row);
+      }
+    };
+
+    auto compute = [&](Tile &T) {
+      // stage V row-major in LDS (rows past the tile are never read)
+#pragma unroll
+      for (int u = 0; u < VLOADS; ++u) {
+        if (TILE * PIECES % 64 == 0 || u * 64 + lane < TILE * PIECES)
+          *reinterpret_cast<v4u32 *>(vtile + v_lds[u]) = T.v[u];
+      }
+      // S^T for tokens 4g + i and head hl
+      f32x4_t sa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) sa = ops::mma_k32(T.k[s], qb[s], sa);
+      float sc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[i] = sa[i] * p.scale_log2;
+        if (T.n_valid < TILE) sc[i] = 4 * grp + i < T.n_valid ? sc[i] : -INFINITY;
+      }
+      float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      tmax = max_xor32(max_xor16(tmax));
+      const bool need = tmax > m + RESCALE_LOG2;
+      if (__builtin_amdgcn_ballot_w64(need) != 0ull) {
+        const float alpha = need ? fast_exp2(m - tmax) : 1.f;
+        m = need ? tmax : m;
+        lsum *= alpha;
+#pragma unroll
+        for (int mt = 0; mt < MTILES; ++mt) acc[mt] *= alpha;
+      }
+      float pr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pr[i] = fast_exp2(sc[i] - m);
+        lsum += pr[i];
+      }
+      const u32x2_t pb = {ops::pack(pr[0], pr[1]), ops::pack(pr[2], pr[3])};
+      // O^T += V^T P
+#pragma unroll
+      for (int mt = 0; mt < MTILES; ++mt) {
+        typedef __attribute__((address_space(3))) s16x4_t *lds_s4_ptr;
+        const s16x4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_ptr)(vtile + tr_lds[mt]));
+        acc[mt] = ops::mma_k16(__builtin_bit_cast(u32x2_t, va), pb, acc[mt]);
+      }
+    };
+
+    // software pipeline: the loads of the next IKL_MFMA_PREFETCH tiles fly
+    // while a tile computes
+#if IKL_MFMA_PREFETCH == 2
+    Tile ta, tb, tc;
+    issue(0, ta);
+    issue(1, tb);
+    for (int t = 0; t < n_tiles; t += 3) {
+      issue(t + 2, tc);
+      compute(ta);
+      issue(t + 3, ta);
+      if (t + 1 < n_tiles) compute(tb);
+      issue(t + 4, tb);
+      if (t + 2 < n_tiles) compute(tc);
+    }
+#else
+    Tile ta, tb;
+    issue(0, ta);
+    for (int t = 0; t < n_tiles; t += 2) {
+      issue(t + 1, tb);
+      compute(ta);
+      issue(t + 2, ta);
+      if (t + 1 < n_tiles) compute(tb);
+    }
+#endif
+    // combine the four lane groups' sums (m is already common to them)
+    lsum = sum_xor32(sum_xor16(lsum));
+  }
+
+  // Writes acc * f as rows [head hl][dims] of a [16][SROW] fp32 block.
+  __device__ __forceinline__ void stage(float *blk, float f, bool head_ok) const {
+    if (!head_ok) return;
+#pragma unroll
+    for (int mt = 0; mt < MTILES; ++mt)
+      *reinterpret_cast<f32x4_t *>(blk + hl * SROW + 16 * mt + 4 * grp) = acc[mt] * f;
+  }
+};
+
+// Sum of NSUM staged [16][D + 4] blocks (stride 16 * (D + 4) floats) at
+// head h, dims d .. d + 3.
+template <int D, int NSUM>
+__device__ __forceinline__ f32x4_t gather4(const float *st, int h, int d) {
+  constexpr int SROW = D + 4;
+  f32x4_t v = *reinterpret_cast<const f32x4_t *>(st + h * SROW + d);
+#pragma unroll
+  for (int w = 1; w < NSUM; ++w) v += *reinterpret_cast<const f32x4_t *>(st + w * 16 * SROW + h * SROW + d);
+  return v;
+}
+
+// nh rows of D fp32 (contiguous) from the staged blocks, 16 bytes a thread.
+template <int D, int NSUM>
+__device__ __forceinline__ void store_rows_f32(float *dst, const float *st, int nh, int tid, int nthreads) {
+  for (int i = tid; i < nh * D / 4; i += nthreads)
+    *reinterpret_cast<f32x4_t *>(dst + 4 * i) = gather4<D, NSUM>(st, 4 * i / D, 4 * i % D);
+}
+
+// nh output rows (heads hq0.., stride o_sh elements) of request b, rounded
+// to the output dtype, 16 bytes a thread.
+template <typename Tag, int D, int NSUM>
+__device__ __forceinline__ void store_rows_out(const AttnParams &p, int64_t b, int64_t hq0, const float *st,
+                                               int nh, int tid, int nthreads) {
+  constexpr int CPR = D / 8;  // 16-byte output pieces per head row
+  for (int i = tid; i < nh * CPR; i += nthreads) {
+    const int h = i / CPR, c = i % CPR;
+    const f32x4_t lo = gather4<D, NSUM>(st, h, 8 * c), hi = gather4<D, NSUM>(st, h, 8 * c + 4);
+    const float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    store_out_chunk<Tag>(p.out + (b * p.o_sb + (hq0 + h) * p.o_sh + 8 * c) * 2, v);
+  }
+}
+
+template <typename Tag, int D, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_kernel(const AttnParams p) {
+  static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4, "1, 2 or 4 waves per workgroup");
+  using WT = WaveTiles<Tag, D>;
+  // LDS: each wave's V tile during the loop; at the end each wave's staged
+  // [16 heads x D] block, which the workgroup sums. The uses never overlap.
+  constexpr int SLOT = WT::ST_BYTES > WT::VT_BYTES ? WT::ST_BYTES : WT::VT_BYTES;
+  __shared__ __attribute__((aligned(16))) char lds[WAVES * SLOT];
+  __shared__ float lds_m[WAVES][16], lds_l[WAVES][16];
+
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+#if IKL_MFMA_HEAD_MAJOR
+  const int part = blockIdx.y;
+  const int kvh = blockIdx.x / p.groups_per_kv;
+  const int qg = blockIdx.x % p.groups_per_kv;
+#else
   const int part = blockIdx.x;
   const int kvh = blockIdx.y / p.groups_per_kv;
   const int qg = blockIdx.y % p.groups_per_kv;
+#endif
   const int64_t b = blockIdx.z;
 
   const int64_t ctx = p.lens_i64 ? load_index<int64_t>(p.lens, b) : load_index<int32_t>(p.lens, b);
   const int64_t part_start = (int64_t)part * p.partition_size;
   if (part > 0 && part_start >= ctx) return;
   const int64_t part_end = ctx < part_start + p.partition_size ? ctx : part_start + p.partition_size;
-  const int n_tiles = part_end > part_start ? (int)((part_end - part_start + TILE - 1) / TILE) : 0;
+  // The workgroup's waves take contiguous, equal (+-1) runs of the
+  // partition's tiles: [w_start, w_end) for this wave.
+  const int wg_tiles = part_end > part_start ? (int)((part_end - part_start + TILE - 1) / TILE) : 0;
+  const int t_lo = wave * wg_tiles / WAVES, t_hi = (wave + 1) * wg_tiles / WAVES;
+  const int64_t w_start = part_start + (int64_t)t_lo * TILE;
+  const int64_t w_end = part_end < part_start + (int64_t)t_hi * TILE ? part_end : part_start + (int64_t)t_hi * TILE;
 
-  // ---- Q^T operand: lane l holds q[head0 + l%16][32s + 8(l/16) .. +7]
+  WT wt(p);
   const int head0 = qg * p.group_size;
-  const bool head_ok = (hl < p.group_size) && (head0 + hl < p.heads_per_kv);
-  const int64_t hq = (int64_t)kvh * p.heads_per_kv + head0 + hl;
-  v4u32 qb[KSTEPS];
-#pragma unroll
-  for (int s = 0; s < KSTEPS; ++s) {
-    qb[s] = zero4();
-    if (head_ok) qb[s] = load16v_global(p.q + (b * p.q_sb + hq * p.q_sh + 32 * s + 8 * grp) * EB);
-  }
-
-  // ---- per-lane constant offsets (bytes)
-  const int k_lane = (hl * (int)p.k_st + 8 * grp) * EB;  // token hl, dims 8g.. of each k-step
-  int v_lds[VLOADS], v_lane[VLOADS];
-#pragma unroll
-  for (int u = 0; u < VLOADS; ++u) {
-    const int pi = u * 64 + lane;  // V piece: row pi / PIECES, piece pi % PIECES
-    const int row = pi / PIECES < TILE ? pi / PIECES : TILE - 1, c = pi % PIECES;
-    v_lds[u] = row * ROWB + ((c + row) % PIECES) * 16;
-    v_lane[u] = row * (int)p.v_st * EB + c * 16;
-  }
-  int tr_lds[MTILES];  // V^T reads: token 4g + (l%16)/4, dims 16mt + 4((l%16)%4)
-#pragma unroll
-  for (int mt = 0; mt < MTILES; ++mt) {
-    const int row = 4 * grp + (hl >> 2);
-    const int c = 2 * mt + ((hl & 3) >> 1);
-    tr_lds[mt] = row * ROWB + ((c + row) % PIECES) * 16 + (hl & 1) * 8;
-  }
-
-  const char *kbase = p.kc + (int64_t)kvh * p.k_sh * EB;
-  const char *vbase = p.vc + (int64_t)kvh * p.v_sh * EB;
-  const char *zero_row = reinterpret_cast<const char *>(g_zero_row);
-  const int bs = p.block_size;
-  int64_t win_base = p.bs_shift >= 0 ? (part_start >> p.bs_shift) : part_start / bs;
-  int win = load_table_window(p, b, win_base, lane);
-
-  f32x4_t acc[MTILES];
-#pragma unroll
-  for (int mt = 0; mt < MTILES; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m = NEG_SENTINEL, lsum = 0.f;
-
-  struct Tile {
-    v4u32 k[KSTEPS];
-    v4u32 v[VLOADS];
-    int n_valid;  // tokens of the tile inside the partition with a valid block (0..16)
-  };
-
-  // Resolves tile t's block and issues its K/V loads (straight-line:
-  // masked rows read the zero row).
-  auto issue = [&](int t, Tile &T) {
-    const int64_t base = part_start + (int64_t)t * TILE;
-    const int64_t lb = p.bs_shift >= 0 ? (base >> p.bs_shift) : base / bs;
-    if (lb >= win_base + 64) {
-      win_base = lb;
-      win = load_table_window(p, b, win_base, lane);
-    }
-    const int64_t off = base - lb * bs;
-    const int phys = __builtin_amdgcn_readlane(win, (int)(lb - win_base));
-    int64_t left = part_end - base;
-    T.n_valid = phys < 0 || left <= 0 ? 0 : (left >= TILE ? TILE : (int)left);
-    const int64_t kro = ((int64_t)phys * p.k_sb + off * p.k_st) * EB;
-    const int64_t vro = ((int64_t)phys * p.v_sb + off * p.v_st) * EB;
-    const bool k_ok = hl < T.n_valid;
-    const char *kr = k_ok ? kbase + kro + k_lane : zero_row;
-    const int kstep = k_ok ? 64 : 0;
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) T.k[s] = load16v_stream(kr + s * kstep);
-#pragma unroll
-    for (int u = 0; u < VLOADS; ++u) {
-      const int row = (u * 64 + lane) / PIECES;
-      const bool v_ok = row < T.n_valid;
-      T.v[u] = load16v_stream(v_ok ? vbase + vro + v_lane[u] : zero_row);
-    }
-  };
-
-  auto compute = [&](Tile &T) {
-    // stage V row-major in LDS (rows past the tile are never read)
-#pragma unroll
-    for (int u = 0; u < VLOADS; ++u) {
-      if (TILE * PIECES % 64 == 0 || u * 64 + lane < TILE * PIECES)
-        *reinterpret_cast<v4u32 *>(vtile + v_lds[u]) = T.v[u];
-    }
-    // S^T for tokens 4g + i and head hl
-    f32x4_t sa = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) sa = ops::mma_k32(T.k[s], qb[s], sa);
-    float sc[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sc[i] = sa[i] * p.scale_log2;
-      if (T.n_valid < TILE) sc[i] = 4 * grp + i < T.n_valid ? sc[i] : -INFINITY;
-    }
-    float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-    tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
-    tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
-    const bool need = tmax > m + RESCALE_LOG2;
-    if (__builtin_amdgcn_ballot_w64(need) != 0ull) {
-      const float alpha = need ? fast_exp2(m - tmax) : 1.f;
-      m = need ? tmax : m;
-      lsum *= alpha;
-#pragma unroll
-      for (int mt = 0; mt < MTILES; ++mt) acc[mt] *= alpha;
-    }
-    float pr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      pr[i] = fast_exp2(sc[i] - m);
-      lsum += pr[i];
-    }
-    const u32x2_t pb = {ops::pack(pr[0], pr[1]), ops::pack(pr[2], pr[3])};
-    // O^T += V^T P
-#pragma unroll
-    for (int mt = 0; mt < MTILES; ++mt) {
-      typedef __attribute__((address_space(3))) s16x4_t *lds_s4_ptr;
-      const s16x4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_ptr)(vtile + tr_lds[mt]));
-      acc[mt] = ops::mma_k16(__builtin_bit_cast(u32x2_t, va), pb, acc[mt]);
-    }
-  };
-
-  // ---- software pipeline: the loads of the next IKL_MFMA_PREFETCH tiles
-  // fly while a tile computes
-#if IKL_MFMA_PREFETCH == 2
-  Tile ta, tb, tc;
-  issue(0, ta);
-  issue(1, tb);
-  for (int t = 0; t < n_tiles; t += 3) {
-    issue(t + 2, tc);
-    compute(ta);
-    issue(t + 3, ta);
-    if (t + 1 < n_tiles) compute(tb);
-    issue(t + 4, tb);
-    if (t + 2 < n_tiles) compute(tc);
-  }
-#else
-  Tile ta, tb;
-  issue(0, ta);
-  for (int t = 0; t < n_tiles; t += 2) {
-    issue(t + 1, tb);
-    compute(ta);
-    issue(t + 2, ta);
-    if (t + 1 < n_tiles) compute(tb);
-  }
-#endif
-
-  // ---- combine the four groups' partial sums (m is already common)
-  lsum += shfl_xor_f(lsum, 16);
-  lsum += shfl_xor_f(lsum, 32);
-  // Stage the normalised [heads x D] block in LDS so all 64 lanes store
-  // whole 16-byte pieces: the wave's heads are contiguous in the output
-  // and in the [B, NP, H, D] partials.
-  const int nh = p.group_size < p.heads_per_kv - head0 ? p.group_size : p.heads_per_kv - head0;
-  const float inv = p.split ? (lsum > 0.f ? 1.f / lsum : 0.f) : 1.f / lsum;  // 0/0 -> NaN like the reference
-  float *stage = reinterpret_cast<float *>(vtile);
-  if (head_ok) {
-#pragma unroll
-    for (int mt = 0; mt < MTILES; ++mt) {
-      const f32x4_t o = acc[mt] * inv;
-      *reinterpret_cast<f32x4_t *>(stage + hl * D + 16 * mt + 4 * grp) = o;
-    }
-  }
+  const bool head_ok = (wt.hl < p.group_size) && (head0 + wt.hl < p.heads_per_kv);
   const int64_t hq0 = (int64_t)kvh * p.heads_per_kv + head0;
+  wt.load_q(p, b, hq0 + wt.hl, head_ok);
+  wt.attend(p, b, kvh, w_start, w_end, lds + wave * WT::VT_BYTES);
+
+  // combine the workgroup's waves: common max M per head, rescaled sums
+  float M = wt.m, L = wt.lsum, scale = 1.f;
+  if constexpr (WAVES > 1) {
+    if (wt.grp == 0) {
+      lds_m[wave][wt.hl] = wt.m;
+      lds_l[wave][wt.hl] = wt.lsum;
+    }
+    __syncthreads();  // also ends every wave's use of its V tile
+    M = lds_m[0][wt.hl];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) M = fmaxf(M, lds_m[w][wt.hl]);
+    L = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) L += lds_l[w][wt.hl] * fast_exp2(lds_m[w][wt.hl] - M);
+    scale = fast_exp2(wt.m - M);
+  }
+
+  // Each wave stages its rescaled, normalised block; the workgroup sums the
+  // blocks and stores whole 16-byte pieces (the heads are contiguous in the
+  // output and in the [B, NP, H, D] partials).
+  const int nh = p.group_size < p.heads_per_kv - head0 ? p.group_size : p.heads_per_kv - head0;
+  const float inv = p.split ? (L > 0.f ? 1.f / L : 0.f) : 1.f / L;  // 0/0 -> NaN like the reference
+  float *const stage = reinterpret_cast<float *>(lds);
+  wt.stage(stage + wave * 16 * WT::SROW, scale * inv, head_ok);
+  if constexpr (WAVES > 1) __syncthreads();
+  else __builtin_amdgcn_wave_barrier();
   if (p.split) {
     const int64_t prow = (b * p.num_parts + part) * p.num_heads + hq0;
-    float *dst = p.part_o + prow * D;
-    for (int i = lane; i < nh * D / 4; i += 64)
-      *reinterpret_cast<f32x4_t *>(dst + 4 * i) = *reinterpret_cast<const f32x4_t *>(stage + 4 * i);
-    if (head_ok && grp == 0) p.part_lse[prow + hl] = lsum > 0.f ? m + log2f(lsum) : -INFINITY;
+    store_rows_f32<D, WAVES>(p.part_o + prow * D, stage, nh, threadIdx.x, 64 * WAVES);
+    if (wave == 0 && head_ok && wt.grp == 0) p.part_lse[prow + wt.hl] = L > 0.f ? M + log2f(L) : -INFINITY;
   } else {
-    constexpr int CPR = D / 8;  // 16-byte output pieces per head row
-    for (int i = lane; i < nh * CPR; i += 64) {
-      const int h = i / CPR, c = i % CPR;
-      const float *src = stage + h * D + 8 * c;
-      u32x4 w;
-      if constexpr (__is_same(Tag, bf16_tag)) {
-        w.x = elem<bf16_tag>::pack2(src[0], src[1]);
-        w.y = elem<bf16_tag>::pack2(src[2], src[3]);
-        w.z = elem<bf16_tag>::pack2(src[4], src[5]);
-        w.w = elem<bf16_tag>::pack2(src[6], src[7]);
-      } else {
-        w.x = elem<f16_tag>::pack2(src[0], src[1]);
-        w.y = elem<f16_tag>::pack2(src[2], src[3]);
-        w.z = elem<f16_tag>::pack2(src[4], src[5]);
-        w.w = elem<f16_tag>::pack2(src[6], src[7]);
-      }
-      store16(p.out + (b * p.o_sb + (hq0 + h) * p.o_sh + 8 * c) * EB, w);
+    store_rows_out<Tag, D, WAVES>(p, b, hq0, stage, nh, threadIdx.x, 64 * WAVES);
+  }
+}
+
+// Balanced split: one wave per workgroup, p.sk_waves workgroups (grid.x).
+// Wave w attends global tiles [w T / W, (w + 1) T / W) of the batch (T =
+// units x tiles of all requests, W = min(sk_waves, T)) piece by piece — a
+// piece is the part of one (request, unit) inside the run — and writes each
+// piece's normalised output and log2-sum-exp to partial slot unit + w.
+template <typename Tag, int D>
+__global__ __launch_bounds__(64) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_streamk_kernel(const AttnParams p) {
+  using WT = WaveTiles<Tag, D>;
+  constexpr int SLOT = WT::ST_BYTES > WT::VT_BYTES ? WT::ST_BYTES : WT::VT_BYTES;
+  __shared__ __attribute__((aligned(16))) char lds[SLOT];
+  const int lane = threadIdx.x;
+  const int64_t U = p.units;
+
+  // total tiles, then the request holding this wave's first tile
+  int64_t before0;
+  int own0;
+  const int64_t total = request_tiles(p, 0, lane, &before0, &own0);
+  const int64_t T = U * total;
+  const int64_t W = (int64_t)p.sk_waves < T ? (int64_t)p.sk_waves : T;
+  const int64_t w = blockIdx.x;
+  if (w >= W) return;
+  const int64_t g0 = w * T / W, g1 = (w + 1) * T / W;
+
+  int64_t b = -1, pb = 0, base = 0;
+  int nb = 0;
+  for (int64_t c0 = 0; c0 < p.batch && b < 0; c0 += 64) {
+    const int64_t r = c0 + lane;
+    const int n = r < p.batch ? (int)((clamped_ctx(p, r) + 15) >> 4) : 0;
+    const int incl = wave_incl_scan(n, lane);
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(r < p.batch && U * (base + incl) > g0);
+    if (hit) {
+      const int l = __builtin_ctzll(hit);
+      b = c0 + l;
+      nb = __shfl(n, l, 64);
+      pb = base + __shfl(incl, l, 64) - nb;
+    }
+    base += __shfl(incl, 63, 64);
+  }
+
+  WT wt(p);
+  float *const stage = reinterpret_cast<float *>(lds);
+  int64_t g = g0;
+  while (true) {
+    // piece: unit u of request b, request tiles [t_in, t_hi)
+    const int64_t rel = g - U * pb;
+    const int u = (int)(rel / nb);
+    const int64_t t_in = rel - (int64_t)u * nb;
+    const int64_t t_hi = (int64_t)nb < t_in + (g1 - g) ? (int64_t)nb : t_in + (g1 - g);
+    const int kvh = u / p.groups_per_kv, qg = u % p.groups_per_kv;
+    const int head0 = qg * p.group_size;
+    const bool head_ok = (wt.hl < p.group_size) && (head0 + wt.hl < p.heads_per_kv);
+    const int64_t hq0 = (int64_t)kvh * p.heads_per_kv + head0;
+    const int64_t ctx = clamped_ctx(p, b);
+    const int64_t t_end = t_hi * TILE < ctx ? t_hi * TILE : ctx;
+    wt.load_q(p, b, hq0 + wt.hl, head_ok);
+    wt.attend(p, b, kvh, t_in * TILE, t_end, lds);
+
+    const int nh = p.group_size < p.heads_per_kv - head0 ? p.group_size : p.heads_per_kv - head0;
+    const int64_t slot = b * U + u + w;
+    __builtin_amdgcn_wave_barrier();
+    wt.stage(stage, wt.lsum > 0.f ? 1.f / wt.lsum : 0.f, head_ok);
+    __builtin_amdgcn_wave_barrier();
+    store_rows_f32<D, 1>(p.part_o + slot * p.group_size * D, stage, nh, lane, 64);
+    if (head_ok && wt.grp == 0)
+      p.part_lse[slot * p.group_size + wt.hl] = wt.lsum > 0.f ? wt.m + log2f(wt.lsum) : -INFINITY;
+    __builtin_amdgcn_wave_barrier();
+
+    g += t_hi - t_in;
+    if (g >= g1) break;
+    if (t_hi == nb && u == U - 1) {  // next request with tiles (one exists: g < T)
+      do {
+        pb += nb;
+        ++b;
+        nb = (int)((clamped_ctx(p, b) + 15) >> 4);
+      } while (nb == 0);
     }
   }
 }
 
+#ifndef IKL_MFMA_WG_WAVES
+#define IKL_MFMA_WG_WAVES 4
+#endif
+constexpr int WG_WAVES = IKL_MFMA_WG_WAVES;  // waves sharing one partition
+
 template <typename Tag>
 hipError_t launch_dim(int d, const AttnParams &p, dim3 grid, hipStream_t s) {
+  if (p.sk_waves > 0) {
+    const dim3 g((unsigned)p.sk_waves);
+    switch (d) {
+      case 32: paged_decode_mfma_streamk_kernel<Tag, 32><<<g, 64, 0, s>>>(p); break;
+      case 64: paged_decode_mfma_streamk_kernel<Tag, 64><<<g, 64, 0, s>>>(p); break;
+      case 96: paged_decode_mfma_streamk_kernel<Tag, 96><<<g, 64, 0, s>>>(p); break;
+      default: paged_decode_mfma_streamk_kernel<Tag, 128><<<g, 64, 0, s>>>(p); break;
+    }
+    return hipGetLastError();
+  }
+  const dim3 block(64 * WG_WAVES);
+#if IKL_MFMA_HEAD_MAJOR
+  grid = dim3(grid.y, grid.x, grid.z);
+#endif
   switch (d) {
-    case 32: paged_decode_mfma_kernel<Tag, 32><<<grid, 64, 0, s>>>(p); break;
-    case 64: paged_decode_mfma_kernel<Tag, 64><<<grid, 64, 0, s>>>(p); break;
-    case 96: paged_decode_mfma_kernel<Tag, 96><<<grid, 64, 0, s>>>(p); break;
-    default: paged_decode_mfma_kernel<Tag, 128><<<grid, 64, 0, s>>>(p); break;
+    case 32: paged_decode_mfma_kernel<Tag, 32, WG_WAVES><<<grid, block, 0, s>>>(p); break;
+    case 64: paged_decode_mfma_kernel<Tag, 64, WG_WAVES><<<grid, block, 0, s>>>(p); break;
+    case 96: paged_decode_mfma_kernel<Tag, 96, WG_WAVES><<<grid, block, 0, s>>>(p); break;
+    default: paged_decode_mfma_kernel<Tag, 128, WG_WAVES><<<grid, block, 0, s>>>(p); break;
   }
   return hipGetLastError();
+}
+
+// Resident one-wave workgroups of the balanced-split kernel on the current
+// device (CUs x workgroups per CU), cached per device; 2048 (256 CUs x 8)
+// when no device answers (planning on a host without a GPU).
+template <typename Tag, int D>
+int streamk_capacity_for() {
+  constexpr int MAX_DEV = 64;
+  static int cache[MAX_DEV] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) {
+    (void)hipGetLastError();
+    return 2048;
+  }
+  if (cache[dev] > 0) return cache[dev];
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_mfma_streamk_kernel<Tag, D>, 64, 0) !=
+          hipSuccess ||
+      cus <= 0 || per_cu <= 0) {
+    (void)hipGetLastError();
+    return 2048;
+  }
+  cache[dev] = cus * per_cu;
+  return cache[dev];
 }
 
 }  // namespace
@@ -329,6 +537,16 @@ bool mfma_supported(int dtype, int head_dim, int block_size, int group_size) {
 hipError_t launch_mfma_attention(int dtype, int head_dim, const AttnParams &p, dim3 grid, hipStream_t s) {
   if (dtype == IKL_BF16) return launch_dim<bf16_tag>(head_dim, p, grid, s);
   return launch_dim<f16_tag>(head_dim, p, grid, s);
+}
+
+int mfma_streamk_capacity(int dtype, int head_dim) {
+  const bool bf = dtype == IKL_BF16;
+  switch (head_dim) {
+    case 32: return bf ? streamk_capacity_for<bf16_tag, 32>() : streamk_capacity_for<f16_tag, 32>();
+    case 64: return bf ? streamk_capacity_for<bf16_tag, 64>() : streamk_capacity_for<f16_tag, 64>();
+    case 96: return bf ? streamk_capacity_for<bf16_tag, 96>() : streamk_capacity_for<f16_tag, 96>();
+    default: return bf ? streamk_capacity_for<bf16_tag, 128>() : streamk_capacity_for<f16_tag, 128>();
+  }
 }
 
 }  // namespace ikl

@@ -444,7 +444,24 @@ class PreparedPagedAttention:
         self._args.workspace = self.workspace.data_ptr()
         self._args.workspace_bytes = ws
         self.partition_size = self._lib.ikl_paged_attention_partition_size(ctypes.byref(self._args))
+        a = self._args
+        self.path = _PATH_NAMES[self._lib.ikl_paged_attention_path(
+            a.dtype, a.head_dim, a.block_size, a.table_width, a.num_heads // a.num_kv_heads,
+            a.query_group_size)]
+        # The MFMA family's automatic split is the balanced one whenever it
+        # splits (the library falls back to fixed partitions only for
+        # tables mapping >= 2^29 positions).
+        self.balanced_split = (self.path == "mfma_grouped" and not partition_size and ws > 0
+                               and a.table_width * a.block_size < (1 << 29))
         self.device = query.device
+
+    def kernel_names(self) -> tuple[str, str | None]:
+        """(attention kernel, reduce kernel or None) this launch enqueues."""
+        if self.path == "mfma_grouped":
+            main = "paged_decode_mfma_streamk_kernel" if self.balanced_split else "paged_decode_mfma_kernel"
+        else:
+            main = "paged_decode_scalar_kernel"
+        return main, ("paged_decode_reduce_kernel" if self._args.workspace_bytes > 0 else None)
 
     def __call__(self, events=None) -> torch.Tensor:
         for i in range(3):

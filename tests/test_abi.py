@@ -70,9 +70,27 @@ def test_partition_planning_for_the_gqa_decode_shape():
     a = _args(partition_size=-1, max_context_len=8192)
     assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 0
     assert lib.ikl_paged_attention_workspace_size(ctypes.byref(a)) == 0
-    # automatic: short contexts with few workgroups shrink the partition
-    a = _args(partition_size=0, max_context_len=512, batch=16, num_kv_heads=32)
+    # automatic on the scalar family: short contexts with few workgroups
+    # shrink the fixed partition
+    a = _args(partition_size=0, max_context_len=512, batch=16, num_kv_heads=32, dtype=_lib.IKL_F32)
     assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 128
+
+
+def test_balanced_split_planning_on_the_mfma_family():
+    """partition_size=0 on bf16 GQA: the balanced split over W resident
+    waves; the workspace holds (units + W) slots of group_size rows."""
+    lib = _lib.load()
+    a = _args(partition_size=0, max_context_len=8192)
+    part = lib.ikl_paged_attention_partition_size(ctypes.byref(a))
+    ws = lib.ikl_paged_attention_workspace_size(ctypes.byref(a))
+    units, group, tiles = 32 * 8, 4, 32 * 8 * 512
+    assert part > 0 and part % 16 == 0
+    waves = -(-tiles // (part // 16))  # lower bound on W from the longest run
+    assert ws >= (units + waves) * group * (128 * 4 + 4)
+    if not torch.cuda.is_available():  # planning without a device assumes 256 CUs x 8 waves
+        assert part == 16 * (tiles // 2048)
+        rows = (units + 2048) * group
+        assert ws == -(-(rows * 128 * 4) // 256) * 256 + rows * 4
 
 
 def test_invalid_arguments_report_errors():

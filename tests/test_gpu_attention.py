@@ -175,3 +175,92 @@ def test_repeat_runs_are_bit_identical():
     b = ops.paged_decode_attention_hip(*args)
     torch.cuda.synchronize()
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+# ---------------------------------------------------------------- balanced split
+# partition_size=None on the MFMA family runs the balanced split: the batch's
+# tiles are cut into one equal run per resident wave and merged per unit.
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_balanced_split_more_than_64_requests(dtype):
+    """70 requests: the in-kernel request scan walks two 64-request chunks."""
+    gen = np.random.default_rng(40)
+    lengths = [int(x) for x in gen.integers(1, 700, size=70)]
+    lengths[0], lengths[63], lengths[64], lengths[69] = 1, 16, 17, 1000
+    case = make_case(batch=70, num_heads=16, num_kv_heads=4, head_dim=128, block_size=16,
+                     lengths=lengths, dtype=dtype, seed=41)
+    _check(case, "paged_decode_attention_hip", label="sk-70")
+
+
+def test_balanced_split_one_unit_across_many_waves():
+    """One MQA request of 20000 tokens: 1250 tiles, one unit split over ~1250 waves."""
+    case = make_case(batch=1, num_heads=8, num_kv_heads=1, head_dim=128, block_size=32,
+                     lengths=[20000], dtype="bfloat16", seed=42)
+    _check(case, "paged_decode_attention_hip", label="sk-long")
+
+
+@pytest.mark.parametrize("lengths", [[1], [1, 1, 1], [15, 16, 17, 33]])
+def test_balanced_split_fewer_tiles_than_waves(lengths):
+    case = make_case(batch=len(lengths), num_heads=8, num_kv_heads=2, head_dim=64, block_size=16,
+                     lengths=lengths, dtype="float16", seed=43)
+    _check(case, "paged_decode_attention_hip", label="sk-tiny")
+
+
+@pytest.mark.parametrize("partition_size", [None, 256])
+def test_empty_contexts_give_nan_rows_and_leave_others_exact(partition_size):
+    """validate_inputs=False with zero-length requests: their rows are NaN
+    (0/0, as the reference's softmax over nothing) in both split modes; the
+    other requests match the oracle."""
+    from inferkernellab_amd import ops
+
+    case = make_case(batch=4, num_heads=32, num_kv_heads=8, head_dim=128, block_size=16,
+                     lengths=[300, 1, 900, 64], dtype="bfloat16", seed=44)
+    lens = case.device_lengths()
+    lens[1] = 0
+    lens[3] = 0
+    out = ops.paged_decode_attention_hip(case.device_query(), case.device_cache(), case.device_tables(),
+                                         lens, validate_inputs=False, partition_size=partition_size)
+    torch.cuda.synchronize()
+    assert torch.isnan(out[1].float()).all() and torch.isnan(out[3].float()).all()
+    expected = case.expected()
+    for b in (0, 2):
+        assert max_abs_err(out[b:b + 1], expected[b:b + 1]) <= ATOL["bfloat16"]
+
+
+@pytest.mark.parametrize("partition_size", [None, 128])
+def test_context_past_table_capacity_is_masked(partition_size):
+    """validate_inputs=False, context_lens beyond the table: positions with no
+    table entry are masked, so the result is attention over the mapped part."""
+    from inferkernellab_amd import ops
+    from oracle import paged_oracle as po
+
+    case = make_case(batch=2, num_heads=8, num_kv_heads=2, head_dim=128, block_size=16,
+                     lengths=[64, 100], dtype="bfloat16", seed=45)
+    # request 0: 4 own blocks, then 3 written blocks of request 1 -> the
+    # table maps 7 * 16 = 112 positions, all holding data
+    row0 = list(case.tables[0]) + list(case.tables[1][:3])
+    tables = torch.tensor([row0, list(case.tables[1])], dtype=torch.int32, device="cuda")
+    lens = torch.tensor([5000, 100], dtype=torch.int32, device="cuda")
+    out = ops.paged_decode_attention_hip(case.device_query(), case.device_cache(), tables, lens,
+                                         validate_inputs=False, partition_size=partition_size)
+    torch.cuda.synchronize()
+    k0, v0 = case.oracle_cache.read(0, row0, 112)
+    ref0 = po.dense_decode_attention(case.query_f32[0:1], po.to_f32(k0, case.dtype), po.to_f32(v0, case.dtype))
+    assert max_abs_err(out[0:1], ref0) <= ATOL["bfloat16"]
+    assert max_abs_err(out[1:2], case.expected()[1:2]) <= ATOL["bfloat16"]
+
+
+def test_balanced_and_fixed_partitions_agree():
+    from inferkernellab_amd import ops
+
+    case = make_case(batch=8, num_heads=32, num_kv_heads=8, head_dim=128, block_size=16,
+                     lengths=[4096, 17, 8192, 5000, 1, 6000, 333, 7777], dtype="bfloat16", seed=46)
+    cache = case.device_cache()
+    args = (case.device_query(), cache, case.device_tables(), case.device_lengths())
+    a = ops.paged_decode_attention_hip(*args)
+    b = ops.paged_decode_attention_hip(*args, partition_size=512)
+    torch.cuda.synchronize()
+    expected = case.expected()
+    assert max_abs_err(a, expected) <= ATOL["bfloat16"]
+    assert max_abs_err(b, expected) <= ATOL["bfloat16"]
+    assert (a.float() - b.float()).abs().max().item() <= ATOL["bfloat16"]
