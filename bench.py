@@ -200,6 +200,9 @@ def main() -> int:
     parser.add_argument("--cpu-budget-s", type=float, default=15.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--seed", type=int, default=0)
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="run only a plain 512 MiB device copy (torch copy_) three times: the "
+                             "known-size reference for scaling FETCH_SIZE / WRITE_SIZE counters")
     args = parser.parse_args()
 
     if args.gpus != 1:
@@ -210,10 +213,20 @@ def main() -> int:
         print(json.dumps({"error": "no GPU visible"}))
         return 2
 
-    from inferkernellab_amd import ops
-
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
+    if args.copy_calibration:
+        nbytes = 512 << 20
+        src = torch.ones(nbytes // 4, dtype=torch.int32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration": {"bytes_read": nbytes, "bytes_written": nbytes, "launches": 3}}))
+        return 0
+
+    from inferkernellab_amd import ops
+
     w = build_workload(args.workload, device, args.seed)
     partition = args.partition_size or WORKLOADS[args.workload][9]
     attn = ops.PreparedPagedAttention(
