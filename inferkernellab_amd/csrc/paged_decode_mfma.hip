@@ -52,6 +52,9 @@ constexpr int TILE = 16;  // tokens per tile
 
 // Tuning knobs: tiles prefetched ahead of the one computing (1 or 2), and an
 // optional minimum-occupancy request to the register allocator.
+#ifndef IKL_MFMA_SPLIT_P
+#define IKL_MFMA_SPLIT_P 1
+#endif
 #ifndef IKL_MFMA_HEAD_MAJOR
 #define IKL_MFMA_HEAD_MAJOR 1
 #endif
@@ -83,6 +86,9 @@ struct mfma_ops<bf16_tag> {
   __device__ static inline uint32_t pack(float x, float y) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{x, y}, bf16x2_t));
   }
+  __device__ static inline float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  __device__ static inline float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  static constexpr bool SPLIT_P = IKL_MFMA_SPLIT_P != 0;
 };
 
 template <>
@@ -98,6 +104,9 @@ struct mfma_ops<f16_tag> {
   __device__ static inline uint32_t pack(float x, float y) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{x, y}, f16x2_t));
   }
+  __device__ static inline float lo(uint32_t w) { return (float)__builtin_bit_cast(f16x2_t, w)[0]; }
+  __device__ static inline float hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2_t, w)[1]; }
+  static constexpr bool SPLIT_P = false;  // fp16 P (<= 2^8) already keeps 11 bits
 };
 
 __device__ inline v4u32 zero4() { return v4u32{0u, 0u, 0u, 0u}; }
@@ -239,12 +248,22 @@ struct WaveTiles {
         lsum += pr[i];
       }
       const u32x2_t pb = {ops::pack(pr[0], pr[1]), ops::pack(pr[2], pr[3])};
-      // O^T += V^T P
+      // O^T += V^T P. A bf16 P keeps 8 significant bits; with IKL_MFMA_SPLIT_P
+      // the rounding residual P - bf16(P) goes through a second MFMA, so P
+      // enters with ~16 bits (as the fp32 P of the reference's kernels).
+      s16x4_t va[MTILES];
 #pragma unroll
       for (int mt = 0; mt < MTILES; ++mt) {
         typedef __attribute__((address_space(3))) s16x4_t *lds_s4_ptr;
-        const s16x4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_ptr)(vtile + tr_lds[mt]));
-        acc[mt] = ops::mma_k16(__builtin_bit_cast(u32x2_t, va), pb, acc[mt]);
+        va[mt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_ptr)(vtile + tr_lds[mt]));
+        acc[mt] = ops::mma_k16(__builtin_bit_cast(u32x2_t, va[mt]), pb, acc[mt]);
+      }
+      if constexpr (ops::SPLIT_P) {
+        const u32x2_t pl = {ops::pack(pr[0] - ops::lo(pb.x), pr[1] - ops::hi(pb.x)),
+                            ops::pack(pr[2] - ops::lo(pb.y), pr[3] - ops::hi(pb.y))};
+#pragma unroll
+        for (int mt = 0; mt < MTILES; ++mt)
+          acc[mt] = ops::mma_k16(__builtin_bit_cast(u32x2_t, va[mt]), pl, acc[mt]);
       }
     };
 
