@@ -169,6 +169,25 @@ int32_t ikl_paged_attention_path(int32_t dtype, int32_t head_dim, int32_t block_
                                  int64_t table_width, int32_t heads_per_kv,
                                  int32_t query_group_size);
 
+/* Resolved launch of an ikl_paged_attention call (filled by
+ * ikl_paged_attention_launch_config). */
+typedef struct ikl_launch_config {
+  int32_t path;                /* enum ikl_attention_path */
+  int32_t tile_tokens;         /* positions one wave takes per loop step */
+  int32_t waves_per_workgroup;
+  int32_t stages;              /* tiles in flight per wave (software pipeline depth) */
+  int32_t split;               /* 0 = none, 1 = fixed partitions, 2 = balanced split */
+  int32_t partition_size;      /* as ikl_paged_attention_partition_size */
+  int64_t workgroups;          /* grid size of the attention kernel */
+} ikl_launch_config;
+
+/* Launch configuration `args` resolves to, without launching. Replaces the
+ * autotune-config reporters of triton_ops.py:17-53 (block_n / num_warps /
+ * num_stages of the last autotuned launch): these kernels are not
+ * autotuned, their configuration follows from the arguments. Returns 0 or
+ * a negative IKL_E* code. */
+int ikl_paged_attention_launch_config(const ikl_paged_attention_args *args, ikl_launch_config *out);
+
 #ifdef __cplusplus
 }
 #endif

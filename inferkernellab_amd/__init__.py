@@ -2,7 +2,9 @@
 
 Hand-written HIP kernels (KV append, paged decode attention with split
 partitions) behind the C ABI of include/ikl_paged.h, with the reference's
-operator surface (ops), paged cache (cache), scheduler and runtime hooks.
+operator surface (ops), paged cache (cache), scheduler and runtime hooks,
+and the decode runners that call them (decode: synthetic decoder; llama:
+Llama over the paged cache).
 """
 
 from .cache import BlockAllocator, CacheLayout, PagedKVCache
@@ -15,6 +17,9 @@ from .ops import (
     paged_decode_attention_hip_grouped,
     paged_decode_attention_triton,
     paged_decode_attention_triton_grouped,
+    paged_decode_autotune_config,
+    paged_decode_grouped_autotune_config,
+    paged_decode_grouped_dot_autotune_config,
     paged_decode_grouped_path,
     triton_append_available,
     triton_available,
@@ -40,6 +45,9 @@ __all__ = [
     "paged_decode_attention_triton",
     "paged_decode_attention_triton_grouped",
     "paged_decode_grouped_path",
+    "paged_decode_autotune_config",
+    "paged_decode_grouped_autotune_config",
+    "paged_decode_grouped_dot_autotune_config",
     "triton_available",
     "triton_append_available",
 ]

@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "ikl_paged_attention_partition_size",
     "ikl_paged_attention",
     "ikl_paged_attention_path",
+    "ikl_paged_attention_launch_config",
 )
 
 _c_i64 = ctypes.c_int64
@@ -109,6 +110,20 @@ class PagedAttentionArgs(ctypes.Structure):
     ]
 
 
+class LaunchConfig(ctypes.Structure):
+    """Mirror of ikl_launch_config."""
+
+    _fields_ = [
+        ("path", _c_i32),
+        ("tile_tokens", _c_i32),
+        ("waves_per_workgroup", _c_i32),
+        ("stages", _c_i32),
+        ("split", _c_i32),
+        ("partition_size", _c_i32),
+        ("workgroups", _c_i64),
+    ]
+
+
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
 _load_error: str | None = None
@@ -129,6 +144,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ikl_paged_attention.argtypes = [ctypes.POINTER(PagedAttentionArgs), _c_ptr]
     lib.ikl_paged_attention_path.restype = _c_i32
     lib.ikl_paged_attention_path.argtypes = [_c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32]
+    lib.ikl_paged_attention_launch_config.restype = ctypes.c_int
+    lib.ikl_paged_attention_launch_config.argtypes = [ctypes.POINTER(PagedAttentionArgs),
+                                                      ctypes.POINTER(LaunchConfig)]
 
 
 def load() -> ctypes.CDLL:

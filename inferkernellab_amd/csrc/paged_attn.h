@@ -160,8 +160,14 @@ __device__ inline int64_t wave_of_tile(int64_t g, int64_t T, int64_t W) { return
 // p.sk_waves one-wave workgroups for the balanced split).
 bool mfma_supported(int dtype, int head_dim, int block_size, int group_size);
 hipError_t launch_mfma_attention(int dtype, int head_dim, const AttnParams &p, dim3 grid, hipStream_t s);
-// One-wave workgroups of the balanced-split MFMA kernel resident at once on
-// the current device (the split's wave count).
-int mfma_streamk_capacity(int dtype, int head_dim);
+// Static launch shape of the MFMA family (fixed partitions or balanced split).
+struct MfmaShape {
+  int tile_tokens, waves_per_workgroup, stages;
+};
+MfmaShape mfma_launch_shape(bool balanced, int group_size);
+
+// One-wave workgroups of the balanced-split MFMA kernel (for units of
+// `group_size` heads) resident at once on the current device.
+int mfma_streamk_capacity(int dtype, int head_dim, int group_size);
 
 }  // namespace ikl

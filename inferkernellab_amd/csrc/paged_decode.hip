@@ -436,7 +436,7 @@ int next_pow2(int x) {
 }
 
 constexpr int SCALAR_MAX_GROUP = 8;
-constexpr int MFMA_MAX_GROUP = 16;
+constexpr int MFMA_MAX_GROUP = 32;
 
 // Kernel family of a launch shape: one query head per KV head -> the
 // one-head scalar kernel; fp16/bf16 with an MFMA-compatible head_dim and
@@ -504,7 +504,7 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
   // (T + 1) * W to fit in 63 bits.
   if (a->partition_size == 0 && pl.path == IKL_PATH_MFMA_GROUPED && cap < (int64_t(1) << 29)) {
     const int64_t t_max = units * ((maxctx + 15) / 16);
-    const int64_t w = std::min<int64_t>(mfma_streamk_capacity(a->dtype, a->head_dim), std::max<int64_t>(t_max, 1));
+    const int64_t w = std::min<int64_t>(mfma_streamk_capacity(a->dtype, a->head_dim, pl.group_size), std::max<int64_t>(t_max, 1));
     if ((double)(t_max + 1) * (double)w < 4.0e18) {
       pl.sk_waves = (int)w;
       pl.split = true;
@@ -612,6 +612,59 @@ extern "C" int32_t ikl_paged_attention_partition_size(const ikl_paged_attention_
   int rc = make_plan(a, pl);
   if (rc != IKL_OK) return rc;
   return pl.split ? pl.partition : 0;
+}
+
+namespace ikl {
+namespace {
+template <typename Tag, int D>
+int scalar_tile_tokens(int gmax) {
+  switch (gmax) {
+    case 1: return ScalarCfg<Tag, D, 1>::TI;
+    case 2: return ScalarCfg<Tag, D, 2>::TI;
+    case 4: return ScalarCfg<Tag, D, 4>::TI;
+    default: return ScalarCfg<Tag, D, 8>::TI;
+  }
+}
+template <typename Tag>
+int scalar_tile_tokens_dim(int d, int gmax) {
+  switch (d) {
+    case 16: return scalar_tile_tokens<Tag, 16>(gmax);
+    case 32: return scalar_tile_tokens<Tag, 32>(gmax);
+    case 64: return scalar_tile_tokens<Tag, 64>(gmax);
+    case 96: return scalar_tile_tokens<Tag, 96>(gmax);
+    default: return scalar_tile_tokens<Tag, 128>(gmax);
+  }
+}
+}  // namespace
+}  // namespace ikl
+
+extern "C" int ikl_paged_attention_launch_config(const ikl_paged_attention_args *a, ikl_launch_config *out) {
+  if (!out) return fail(IKL_EINVAL, "launch config: null output struct");
+  Plan pl;
+  int rc = make_plan(a, pl);
+  if (rc != IKL_OK) return rc;
+  ikl_launch_config c{};
+  c.path = pl.path;
+  c.partition_size = pl.split ? pl.partition : 0;
+  if (pl.path == IKL_PATH_MFMA_GROUPED) {
+    const MfmaShape sh = mfma_launch_shape(pl.sk_waves > 0, pl.group_size);
+    c.tile_tokens = sh.tile_tokens;
+    c.waves_per_workgroup = sh.waves_per_workgroup;
+    c.stages = sh.stages;
+  } else {
+    switch (a->dtype) {
+      case IKL_F16: c.tile_tokens = scalar_tile_tokens_dim<f16_tag>(a->head_dim, pl.gmax); break;
+      case IKL_BF16: c.tile_tokens = scalar_tile_tokens_dim<bf16_tag>(a->head_dim, pl.gmax); break;
+      default: c.tile_tokens = scalar_tile_tokens_dim<f32_tag>(a->head_dim, pl.gmax); break;
+    }
+    c.waves_per_workgroup = 1;
+    c.stages = 2;
+  }
+  c.split = pl.sk_waves > 0 ? 2 : (pl.split ? 1 : 0);
+  c.workgroups = pl.sk_waves > 0 ? (int64_t)pl.sk_waves
+                                 : (int64_t)pl.num_parts * a->num_kv_heads * pl.groups_per_kv * a->batch;
+  *out = c;
+  return IKL_OK;
 }
 
 extern "C" int32_t ikl_paged_attention_path(int32_t dtype, int32_t head_dim, int32_t block_size,

@@ -111,12 +111,17 @@ struct mfma_ops<f16_tag> {
 
 __device__ inline v4u32 zero4() { return v4u32{0u, 0u, 0u, 0u}; }
 
-// Per-wave state of the tile loop: lane constants, the Q^T operand and the
-// running softmax state (acc, m, lsum) of one (request, unit) run.
-template <typename Tag, int D>
+// Per-wave state of the tile loop: lane constants, the Q^T operands and the
+// running softmax states (acc, m, lsum) of one (request, unit) run. A unit
+// has up to NG * 16 query heads: NG 16-head MFMA groups share every K/V tile
+// the wave loads (NG = 2 serves 32-head groups such as MQA-32 without
+// reading K/V twice).
+template <typename Tag, int D, int NG>
 struct WaveTiles {
   static_assert(D % 32 == 0 && D <= 128, "MFMA path needs head_dim = 32k <= 128");
+  static_assert(NG == 1 || NG == 2, "one or two 16-head groups per wave");
   static constexpr int EB = 2;
+  static constexpr int NH = 16 * NG;                        // query heads per wave
   static constexpr int KSTEPS = D / 32;                     // QK^T k-steps
   static constexpr int MTILES = D / 16;                     // PV output tiles of 16 dims
   static constexpr int PIECES = D * EB / 16;                // 16-byte pieces per row
@@ -124,7 +129,7 @@ struct WaveTiles {
   static constexpr int VLOADS = (TILE * PIECES + 63) / 64;  // 16-byte V loads per lane per tile
   static constexpr int VT_BYTES = TILE * ROWB;              // one staged V tile
   static constexpr int SROW = D + 4;                        // staged fp32 row (padded vs bank conflicts)
-  static constexpr int ST_BYTES = 16 * SROW * 4;            // one staged [16 heads x D] block
+  static constexpr int ST_BYTES = NH * SROW * 4;            // one staged [NH heads x D] block
   using ops = mfma_ops<Tag>;
 
   struct Tile {
@@ -136,9 +141,9 @@ struct WaveTiles {
   int lane, hl, grp;
   int k_lane;
   int v_lds[VLOADS], v_lane[VLOADS], tr_lds[MTILES];
-  v4u32 qb[KSTEPS];
-  f32x4_t acc[MTILES];
-  float m, lsum;
+  v4u32 qb[NG][KSTEPS];
+  f32x4_t acc[NG][MTILES];
+  float m[NG], lsum[NG];
 
   __device__ __forceinline__ explicit WaveTiles(const AttnParams &p) {
     lane = threadIdx.x & 63;
@@ -160,12 +165,17 @@ struct WaveTiles {
     }
   }
 
-  // Q^T operand: lane l holds q[hq(l%16)][32s + 8(l/16) .. +7].
-  __device__ __forceinline__ void load_q(const AttnParams &p, int64_t b, int64_t hq, bool head_ok) {
+  // Q^T operands: in group g, lane l holds q[hq0 + 16g + l%16][32s + 8(l/16) .. +7]
+  // (zero for heads >= nh).
+  __device__ __forceinline__ void load_q(const AttnParams &p, int64_t b, int64_t hq0, int nh) {
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      qb[s] = zero4();
-      if (head_ok) qb[s] = load16v_global(p.q + (b * p.q_sb + hq * p.q_sh + 32 * s + 8 * grp) * EB);
+    for (int g = 0; g < NG; ++g) {
+      const int h = 16 * g + hl;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        qb[g][s] = zero4();
+        if (h < nh) qb[g][s] = load16v_global(p.q + (b * p.q_sb + (hq0 + h) * p.q_sh + 32 * s + 8 * grp) * EB);
+      }
     }
   }
 
@@ -175,9 +185,12 @@ struct WaveTiles {
   __device__ __forceinline__ void attend(const AttnParams &p, int64_t b, int kvh, int64_t t0, int64_t t1,
                                          char *vtile) {
 #pragma unroll
-    for (int mt = 0; mt < MTILES; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    m = NEG_SENTINEL;
-    lsum = 0.f;
+    for (int g = 0; g < NG; ++g) {
+#pragma unroll
+      for (int mt = 0; mt < MTILES; ++mt) acc[g][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      m[g] = NEG_SENTINEL;
+      lsum[g] = 0.f;
+    }
     const int n_tiles = t1 > t0 ? (int)((t1 - t0 + TILE - 1) / TILE) : 0;
     const char *kbase = p.kc + (int64_t)kvh * p.k_sh * EB;
     const char *vbase = p.vc + (int64_t)kvh * p.v_sh * EB;
@@ -221,49 +234,63 @@ struct WaveTiles {
         if (TILE * PIECES % 64 == 0 || u * 64 + lane < TILE * PIECES)
           *reinterpret_cast<v4u32 *>(vtile + v_lds[u]) = T.v[u];
       }
-      // S^T for tokens 4g + i and head hl
-      f32x4_t sa = {0.f, 0.f, 0.f, 0.f};
+      // S^T of each group for tokens 4g' + i and head hl
+      f32x4_t sa[NG];
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) sa = ops::mma_k32(T.k[s], qb[s], sa);
-      float sc[4];
+      for (int g = 0; g < NG; ++g) {
+        sa[g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sc[i] = sa[i] * p.scale_log2;
-        if (T.n_valid < TILE) sc[i] = 4 * grp + i < T.n_valid ? sc[i] : -INFINITY;
+        for (int s = 0; s < KSTEPS; ++s) sa[g] = ops::mma_k32(T.k[s], qb[g][s], sa[g]);
       }
-      float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-      tmax = max_xor32(max_xor16(tmax));
-      const bool need = tmax > m + RESCALE_LOG2;
-      if (__builtin_amdgcn_ballot_w64(need) != 0ull) {
-        const float alpha = need ? fast_exp2(m - tmax) : 1.f;
-        m = need ? tmax : m;
-        lsum *= alpha;
+      u32x2_t pb[NG], pl[NG];
 #pragma unroll
-        for (int mt = 0; mt < MTILES; ++mt) acc[mt] *= alpha;
-      }
-      float pr[4];
+      for (int g = 0; g < NG; ++g) {
+        float sc[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pr[i] = fast_exp2(sc[i] - m);
-        lsum += pr[i];
+        for (int i = 0; i < 4; ++i) {
+          sc[i] = sa[g][i] * p.scale_log2;
+          if (T.n_valid < TILE) sc[i] = 4 * grp + i < T.n_valid ? sc[i] : -INFINITY;
+        }
+        float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        tmax = max_xor32(max_xor16(tmax));
+        const bool need = tmax > m[g] + RESCALE_LOG2;
+        if (__builtin_amdgcn_ballot_w64(need) != 0ull) {
+          const float alpha = need ? fast_exp2(m[g] - tmax) : 1.f;
+          m[g] = need ? tmax : m[g];
+          lsum[g] *= alpha;
+#pragma unroll
+          for (int mt = 0; mt < MTILES; ++mt) acc[g][mt] *= alpha;
+        }
+        float pr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pr[i] = fast_exp2(sc[i] - m[g]);
+          lsum[g] += pr[i];
+        }
+        pb[g] = u32x2_t{ops::pack(pr[0], pr[1]), ops::pack(pr[2], pr[3])};
+        // A bf16 P keeps 8 significant bits; with SPLIT_P its rounding
+        // residual P - bf16(P) goes through a second MFMA, so P enters with
+        // ~16 bits (as the fp32 P of the reference's kernels).
+        if constexpr (ops::SPLIT_P)
+          pl[g] = u32x2_t{ops::pack(pr[0] - ops::lo(pb[g].x), pr[1] - ops::hi(pb[g].x)),
+                          ops::pack(pr[2] - ops::lo(pb[g].y), pr[3] - ops::hi(pb[g].y))};
       }
-      const u32x2_t pb = {ops::pack(pr[0], pr[1]), ops::pack(pr[2], pr[3])};
-      // O^T += V^T P. A bf16 P keeps 8 significant bits; with IKL_MFMA_SPLIT_P
-      // the rounding residual P - bf16(P) goes through a second MFMA, so P
-      // enters with ~16 bits (as the fp32 P of the reference's kernels).
+      // O^T += V^T P, every group on the same V^T operand
       s16x4_t va[MTILES];
 #pragma unroll
       for (int mt = 0; mt < MTILES; ++mt) {
         typedef __attribute__((address_space(3))) s16x4_t *lds_s4_ptr;
         va[mt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_ptr)(vtile + tr_lds[mt]));
-        acc[mt] = ops::mma_k16(__builtin_bit_cast(u32x2_t, va[mt]), pb, acc[mt]);
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+          acc[g][mt] = ops::mma_k16(__builtin_bit_cast(u32x2_t, va[mt]), pb[g], acc[g][mt]);
       }
       if constexpr (ops::SPLIT_P) {
-        const u32x2_t pl = {ops::pack(pr[0] - ops::lo(pb.x), pr[1] - ops::hi(pb.x)),
-                            ops::pack(pr[2] - ops::lo(pb.y), pr[3] - ops::hi(pb.y))};
 #pragma unroll
         for (int mt = 0; mt < MTILES; ++mt)
-          acc[mt] = ops::mma_k16(__builtin_bit_cast(u32x2_t, va[mt]), pl, acc[mt]);
+#pragma unroll
+          for (int g = 0; g < NG; ++g)
+            acc[g][mt] = ops::mma_k16(__builtin_bit_cast(u32x2_t, va[mt]), pl[g], acc[g][mt]);
       }
     };
 
@@ -292,59 +319,65 @@ struct WaveTiles {
     }
 #endif
     // combine the four lane groups' sums (m is already common to them)
-    lsum = sum_xor32(sum_xor16(lsum));
+#pragma unroll
+    for (int g = 0; g < NG; ++g) lsum[g] = sum_xor32(sum_xor16(lsum[g]));
   }
 
-  // Writes acc * f as rows [head hl][dims] of a [16][SROW] fp32 block.
-  __device__ __forceinline__ void stage(float *blk, float f, bool head_ok) const {
-    if (!head_ok) return;
+  // Writes acc[g] * f[g] as rows [head 16g + hl][dims] of an [NH][SROW]
+  // fp32 block, for heads < nh.
+  __device__ __forceinline__ void stage(float *blk, const float *f, int nh) const {
 #pragma unroll
-    for (int mt = 0; mt < MTILES; ++mt)
-      *reinterpret_cast<f32x4_t *>(blk + hl * SROW + 16 * mt + 4 * grp) = acc[mt] * f;
+    for (int g = 0; g < NG; ++g) {
+      const int h = 16 * g + hl;
+      if (h >= nh) continue;
+#pragma unroll
+      for (int mt = 0; mt < MTILES; ++mt)
+        *reinterpret_cast<f32x4_t *>(blk + h * SROW + 16 * mt + 4 * grp) = acc[g][mt] * f[g];
+    }
   }
 };
 
-// Sum of NSUM staged [16][D + 4] blocks (stride 16 * (D + 4) floats) at
-// head h, dims d .. d + 3.
-template <int D, int NSUM>
+// Sum of NSUM staged [NH][D + 4] blocks (consecutive) at head h, dims d .. d + 3.
+template <int D, int NH, int NSUM>
 __device__ __forceinline__ f32x4_t gather4(const float *st, int h, int d) {
   constexpr int SROW = D + 4;
   f32x4_t v = *reinterpret_cast<const f32x4_t *>(st + h * SROW + d);
 #pragma unroll
-  for (int w = 1; w < NSUM; ++w) v += *reinterpret_cast<const f32x4_t *>(st + w * 16 * SROW + h * SROW + d);
+  for (int w = 1; w < NSUM; ++w) v += *reinterpret_cast<const f32x4_t *>(st + w * NH * SROW + h * SROW + d);
   return v;
 }
 
 // nh rows of D fp32 (contiguous) from the staged blocks, 16 bytes a thread.
-template <int D, int NSUM>
+template <int D, int NH, int NSUM>
 __device__ __forceinline__ void store_rows_f32(float *dst, const float *st, int nh, int tid, int nthreads) {
   for (int i = tid; i < nh * D / 4; i += nthreads)
-    *reinterpret_cast<f32x4_t *>(dst + 4 * i) = gather4<D, NSUM>(st, 4 * i / D, 4 * i % D);
+    *reinterpret_cast<f32x4_t *>(dst + 4 * i) = gather4<D, NH, NSUM>(st, 4 * i / D, 4 * i % D);
 }
 
 // nh output rows (heads hq0.., stride o_sh elements) of request b, rounded
 // to the output dtype, 16 bytes a thread.
-template <typename Tag, int D, int NSUM>
+template <typename Tag, int D, int NH, int NSUM>
 __device__ __forceinline__ void store_rows_out(const AttnParams &p, int64_t b, int64_t hq0, const float *st,
                                                int nh, int tid, int nthreads) {
   constexpr int CPR = D / 8;  // 16-byte output pieces per head row
   for (int i = tid; i < nh * CPR; i += nthreads) {
     const int h = i / CPR, c = i % CPR;
-    const f32x4_t lo = gather4<D, NSUM>(st, h, 8 * c), hi = gather4<D, NSUM>(st, h, 8 * c + 4);
+    const f32x4_t lo = gather4<D, NH, NSUM>(st, h, 8 * c), hi = gather4<D, NH, NSUM>(st, h, 8 * c + 4);
     const float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     store_out_chunk<Tag>(p.out + (b * p.o_sb + (hq0 + h) * p.o_sh + 8 * c) * 2, v);
   }
 }
 
-template <typename Tag, int D, int WAVES>
+template <typename Tag, int D, int NG, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_kernel(const AttnParams p) {
   static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4, "1, 2 or 4 waves per workgroup");
-  using WT = WaveTiles<Tag, D>;
+  using WT = WaveTiles<Tag, D, NG>;
+  constexpr int NH = WT::NH;
   // LDS: each wave's V tile during the loop; at the end each wave's staged
-  // [16 heads x D] block, which the workgroup sums. The uses never overlap.
+  // [NH heads x D] block, which the workgroup sums. The uses never overlap.
   constexpr int SLOT = WT::ST_BYTES > WT::VT_BYTES ? WT::ST_BYTES : WT::VT_BYTES;
   __shared__ __attribute__((aligned(16))) char lds[WAVES * SLOT];
-  __shared__ float lds_m[WAVES][16], lds_l[WAVES][16];
+  __shared__ float lds_m[WAVES][NH], lds_l[WAVES][NH];
 
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
 #if IKL_MFMA_HEAD_MAJOR
@@ -371,43 +404,60 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
 
   WT wt(p);
   const int head0 = qg * p.group_size;
-  const bool head_ok = (wt.hl < p.group_size) && (head0 + wt.hl < p.heads_per_kv);
+  const int nh = p.group_size < p.heads_per_kv - head0 ? p.group_size : p.heads_per_kv - head0;
   const int64_t hq0 = (int64_t)kvh * p.heads_per_kv + head0;
-  wt.load_q(p, b, hq0 + wt.hl, head_ok);
+  wt.load_q(p, b, hq0, nh);
   wt.attend(p, b, kvh, w_start, w_end, lds + wave * WT::VT_BYTES);
 
   // combine the workgroup's waves: common max M per head, rescaled sums
-  float M = wt.m, L = wt.lsum, scale = 1.f;
+  float M[NG], L[NG], f[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    M[g] = wt.m[g];
+    L[g] = wt.lsum[g];
+  }
   if constexpr (WAVES > 1) {
     if (wt.grp == 0) {
-      lds_m[wave][wt.hl] = wt.m;
-      lds_l[wave][wt.hl] = wt.lsum;
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        lds_m[wave][16 * g + wt.hl] = wt.m[g];
+        lds_l[wave][16 * g + wt.hl] = wt.lsum[g];
+      }
     }
     __syncthreads();  // also ends every wave's use of its V tile
-    M = lds_m[0][wt.hl];
 #pragma unroll
-    for (int w = 1; w < WAVES; ++w) M = fmaxf(M, lds_m[w][wt.hl]);
-    L = 0.f;
+    for (int g = 0; g < NG; ++g) {
+      const int h = 16 * g + wt.hl;
+      M[g] = lds_m[0][h];
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w) L += lds_l[w][wt.hl] * fast_exp2(lds_m[w][wt.hl] - M);
-    scale = fast_exp2(wt.m - M);
+      for (int w = 1; w < WAVES; ++w) M[g] = fmaxf(M[g], lds_m[w][h]);
+      L[g] = 0.f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) L[g] += lds_l[w][h] * fast_exp2(lds_m[w][h] - M[g]);
+    }
   }
-
   // Each wave stages its rescaled, normalised block; the workgroup sums the
   // blocks and stores whole 16-byte pieces (the heads are contiguous in the
   // output and in the [B, NP, H, D] partials).
-  const int nh = p.group_size < p.heads_per_kv - head0 ? p.group_size : p.heads_per_kv - head0;
-  const float inv = p.split ? (L > 0.f ? 1.f / L : 0.f) : 1.f / L;  // 0/0 -> NaN like the reference
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    const float inv = p.split ? (L[g] > 0.f ? 1.f / L[g] : 0.f) : 1.f / L[g];  // 0/0 -> NaN like the reference
+    f[g] = (WAVES > 1 ? fast_exp2(wt.m[g] - M[g]) : 1.f) * inv;
+  }
   float *const stage = reinterpret_cast<float *>(lds);
-  wt.stage(stage + wave * 16 * WT::SROW, scale * inv, head_ok);
+  wt.stage(stage + wave * NH * WT::SROW, f, nh);
   if constexpr (WAVES > 1) __syncthreads();
   else __builtin_amdgcn_wave_barrier();
   if (p.split) {
     const int64_t prow = (b * p.num_parts + part) * p.num_heads + hq0;
-    store_rows_f32<D, WAVES>(p.part_o + prow * D, stage, nh, threadIdx.x, 64 * WAVES);
-    if (wave == 0 && head_ok && wt.grp == 0) p.part_lse[prow + wt.hl] = L > 0.f ? M + log2f(L) : -INFINITY;
+    store_rows_f32<D, NH, WAVES>(p.part_o + prow * D, stage, nh, threadIdx.x, 64 * WAVES);
+    if (wave == 0 && wt.grp == 0) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+        if (16 * g + wt.hl < nh) p.part_lse[prow + 16 * g + wt.hl] = L[g] > 0.f ? M[g] + log2f(L[g]) : -INFINITY;
+    }
   } else {
-    store_rows_out<Tag, D, WAVES>(p, b, hq0, stage, nh, threadIdx.x, 64 * WAVES);
+    store_rows_out<Tag, D, NH, WAVES>(p, b, hq0, stage, nh, threadIdx.x, 64 * WAVES);
   }
 }
 
@@ -416,9 +466,10 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
 // units x tiles of all requests, W = min(sk_waves, T)) piece by piece — a
 // piece is the part of one (request, unit) inside the run — and writes each
 // piece's normalised output and log2-sum-exp to partial slot unit + w.
-template <typename Tag, int D>
+template <typename Tag, int D, int NG>
 __global__ __launch_bounds__(64) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_streamk_kernel(const AttnParams p) {
-  using WT = WaveTiles<Tag, D>;
+  using WT = WaveTiles<Tag, D, NG>;
+  constexpr int NH = WT::NH;
   constexpr int SLOT = WT::ST_BYTES > WT::VT_BYTES ? WT::ST_BYTES : WT::VT_BYTES;
   __shared__ __attribute__((aligned(16))) char lds[SLOT];
   const int lane = threadIdx.x;
@@ -461,21 +512,28 @@ __global__ __launch_bounds__(64) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_stre
     const int64_t t_hi = (int64_t)nb < t_in + (g1 - g) ? (int64_t)nb : t_in + (g1 - g);
     const int kvh = u / p.groups_per_kv, qg = u % p.groups_per_kv;
     const int head0 = qg * p.group_size;
-    const bool head_ok = (wt.hl < p.group_size) && (head0 + wt.hl < p.heads_per_kv);
+    const int nh = p.group_size < p.heads_per_kv - head0 ? p.group_size : p.heads_per_kv - head0;
     const int64_t hq0 = (int64_t)kvh * p.heads_per_kv + head0;
     const int64_t ctx = clamped_ctx(p, b);
     const int64_t t_end = t_hi * TILE < ctx ? t_hi * TILE : ctx;
-    wt.load_q(p, b, hq0 + wt.hl, head_ok);
+    wt.load_q(p, b, hq0, nh);
     wt.attend(p, b, kvh, t_in * TILE, t_end, lds);
 
-    const int nh = p.group_size < p.heads_per_kv - head0 ? p.group_size : p.heads_per_kv - head0;
     const int64_t slot = b * U + u + w;
+    float f[NG];
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) f[gi] = wt.lsum[gi] > 0.f ? 1.f / wt.lsum[gi] : 0.f;
     __builtin_amdgcn_wave_barrier();
-    wt.stage(stage, wt.lsum > 0.f ? 1.f / wt.lsum : 0.f, head_ok);
+    wt.stage(stage, f, nh);
     __builtin_amdgcn_wave_barrier();
-    store_rows_f32<D, 1>(p.part_o + slot * p.group_size * D, stage, nh, lane, 64);
-    if (head_ok && wt.grp == 0)
-      p.part_lse[slot * p.group_size + wt.hl] = wt.lsum > 0.f ? wt.m + log2f(wt.lsum) : -INFINITY;
+    store_rows_f32<D, NH, 1>(p.part_o + slot * p.group_size * D, stage, nh, lane, 64);
+    if (wt.grp == 0) {
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi)
+        if (16 * gi + wt.hl < nh)
+          p.part_lse[slot * p.group_size + 16 * gi + wt.hl] =
+              wt.lsum[gi] > 0.f ? wt.m[gi] + log2f(wt.lsum[gi]) : -INFINITY;
+    }
     __builtin_amdgcn_wave_barrier();
 
     g += t_hi - t_in;
@@ -493,56 +551,71 @@ __global__ __launch_bounds__(64) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_stre
 #ifndef IKL_MFMA_WG_WAVES
 #define IKL_MFMA_WG_WAVES 4
 #endif
-constexpr int WG_WAVES = IKL_MFMA_WG_WAVES;  // waves sharing one partition
+// Waves sharing one fixed partition: 4 for 16-head units; 2 for 32-head
+// units (their staged [32 x D] blocks would exceed 64 KB of LDS at 4).
+template <int NG>
+constexpr int wg_waves() {
+  return NG == 1 ? IKL_MFMA_WG_WAVES : 2;
+}
 
-template <typename Tag>
-hipError_t launch_dim(int d, const AttnParams &p, dim3 grid, hipStream_t s) {
+template <typename Tag, int D, int NG>
+void launch_shape(const AttnParams &p, dim3 grid, hipStream_t s) {
   if (p.sk_waves > 0) {
-    const dim3 g((unsigned)p.sk_waves);
-    switch (d) {
-      case 32: paged_decode_mfma_streamk_kernel<Tag, 32><<<g, 64, 0, s>>>(p); break;
-      case 64: paged_decode_mfma_streamk_kernel<Tag, 64><<<g, 64, 0, s>>>(p); break;
-      case 96: paged_decode_mfma_streamk_kernel<Tag, 96><<<g, 64, 0, s>>>(p); break;
-      default: paged_decode_mfma_streamk_kernel<Tag, 128><<<g, 64, 0, s>>>(p); break;
-    }
-    return hipGetLastError();
+    paged_decode_mfma_streamk_kernel<Tag, D, NG><<<dim3((unsigned)p.sk_waves), 64, 0, s>>>(p);
+    return;
   }
-  const dim3 block(64 * WG_WAVES);
 #if IKL_MFMA_HEAD_MAJOR
   grid = dim3(grid.y, grid.x, grid.z);
 #endif
+  constexpr int WAVES = wg_waves<NG>();
+  paged_decode_mfma_kernel<Tag, D, NG, WAVES><<<grid, dim3(64 * WAVES), 0, s>>>(p);
+}
+
+template <typename Tag, int NG>
+void launch_dim(int d, const AttnParams &p, dim3 grid, hipStream_t s) {
   switch (d) {
-    case 32: paged_decode_mfma_kernel<Tag, 32, WG_WAVES><<<grid, block, 0, s>>>(p); break;
-    case 64: paged_decode_mfma_kernel<Tag, 64, WG_WAVES><<<grid, block, 0, s>>>(p); break;
-    case 96: paged_decode_mfma_kernel<Tag, 96, WG_WAVES><<<grid, block, 0, s>>>(p); break;
-    default: paged_decode_mfma_kernel<Tag, 128, WG_WAVES><<<grid, block, 0, s>>>(p); break;
+    case 32: launch_shape<Tag, 32, NG>(p, grid, s); break;
+    case 64: launch_shape<Tag, 64, NG>(p, grid, s); break;
+    case 96: launch_shape<Tag, 96, NG>(p, grid, s); break;
+    default: launch_shape<Tag, 128, NG>(p, grid, s); break;
   }
-  return hipGetLastError();
 }
 
 // Resident one-wave workgroups of the balanced-split kernel on the current
-// device (CUs x workgroups per CU), cached per device; 2048 (256 CUs x 8)
-// when no device answers (planning on a host without a GPU).
-template <typename Tag, int D>
+// device (CUs x workgroups per CU), cached per device; 256 CUs x the
+// kernel's waves per CU (8 for 16-head units, 4 for 32-head) when no device
+// answers (planning on a host without a GPU).
+template <typename Tag, int D, int NG>
 int streamk_capacity_for() {
   constexpr int MAX_DEV = 64;
+  constexpr int FALLBACK = 256 * (NG == 1 ? 8 : 4);
   static int cache[MAX_DEV] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) {
     (void)hipGetLastError();
-    return 2048;
+    return FALLBACK;
   }
   if (cache[dev] > 0) return cache[dev];
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_mfma_streamk_kernel<Tag, D>, 64, 0) !=
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_mfma_streamk_kernel<Tag, D, NG>, 64, 0) !=
           hipSuccess ||
       cus <= 0 || per_cu <= 0) {
     (void)hipGetLastError();
-    return 2048;
+    return FALLBACK;
   }
   cache[dev] = cus * per_cu;
   return cache[dev];
+}
+
+template <typename Tag, int NG>
+int capacity_dim(int d) {
+  switch (d) {
+    case 32: return streamk_capacity_for<Tag, 32, NG>();
+    case 64: return streamk_capacity_for<Tag, 64, NG>();
+    case 96: return streamk_capacity_for<Tag, 96, NG>();
+    default: return streamk_capacity_for<Tag, 128, NG>();
+  }
 }
 
 }  // namespace
@@ -550,22 +623,30 @@ int streamk_capacity_for() {
 bool mfma_supported(int dtype, int head_dim, int block_size, int group_size) {
   return (dtype == IKL_F16 || dtype == IKL_BF16) &&
          (head_dim == 32 || head_dim == 64 || head_dim == 96 || head_dim == 128) &&
-         block_size > 0 && block_size % 16 == 0 && group_size >= 1 && group_size <= 16;
+         block_size > 0 && block_size % 16 == 0 && group_size >= 1 && group_size <= 32;
 }
 
 hipError_t launch_mfma_attention(int dtype, int head_dim, const AttnParams &p, dim3 grid, hipStream_t s) {
-  if (dtype == IKL_BF16) return launch_dim<bf16_tag>(head_dim, p, grid, s);
-  return launch_dim<f16_tag>(head_dim, p, grid, s);
+  const bool two = p.group_size > 16;
+  if (dtype == IKL_BF16) {
+    if (two) launch_dim<bf16_tag, 2>(head_dim, p, grid, s);
+    else launch_dim<bf16_tag, 1>(head_dim, p, grid, s);
+  } else {
+    if (two) launch_dim<f16_tag, 2>(head_dim, p, grid, s);
+    else launch_dim<f16_tag, 1>(head_dim, p, grid, s);
+  }
+  return hipGetLastError();
 }
 
-int mfma_streamk_capacity(int dtype, int head_dim) {
-  const bool bf = dtype == IKL_BF16;
-  switch (head_dim) {
-    case 32: return bf ? streamk_capacity_for<bf16_tag, 32>() : streamk_capacity_for<f16_tag, 32>();
-    case 64: return bf ? streamk_capacity_for<bf16_tag, 64>() : streamk_capacity_for<f16_tag, 64>();
-    case 96: return bf ? streamk_capacity_for<bf16_tag, 96>() : streamk_capacity_for<f16_tag, 96>();
-    default: return bf ? streamk_capacity_for<bf16_tag, 128>() : streamk_capacity_for<f16_tag, 128>();
-  }
+MfmaShape mfma_launch_shape(bool balanced, int group_size) {
+  const int waves = group_size > 16 ? wg_waves<2>() : wg_waves<1>();
+  return MfmaShape{TILE, balanced ? 1 : waves, IKL_MFMA_PREFETCH + 1};
+}
+
+int mfma_streamk_capacity(int dtype, int head_dim, int group_size) {
+  const bool bf = dtype == IKL_BF16, two = group_size > 16;
+  if (bf) return two ? capacity_dim<bf16_tag, 2>(head_dim) : capacity_dim<bf16_tag, 1>(head_dim);
+  return two ? capacity_dim<f16_tag, 2>(head_dim) : capacity_dim<f16_tag, 1>(head_dim);
 }
 
 }  // namespace ikl

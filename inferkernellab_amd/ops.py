@@ -251,8 +251,62 @@ def _launch_attention(
         stream = torch.cuda.current_stream(query.device).cuda_stream
         status = lib.ikl_paged_attention(ctypes.byref(args), ctypes.c_void_p(stream))
     _lib.check(status, "paged attention")
+    _record_launch(args)
     del keep, workspace  # the caching allocator keeps stream order
     return output
+
+
+# ------------------------------------------------------- launch reporting
+_SPLIT_NAMES = {0: "none", 1: "fixed_partitions", 2: "balanced"}
+_last_launch: dict[str, dict] = {}
+
+
+def launch_config(args) -> dict:
+    """The launch an ikl_paged_attention_args struct resolves to (planning
+    only: needs the library, not a GPU)."""
+    lib = _lib.load()
+    out = _lib.LaunchConfig()
+    _lib.check(lib.ikl_paged_attention_launch_config(ctypes.byref(args), ctypes.byref(out)), "launch config")
+    return {
+        "path": _PATH_NAMES[out.path],
+        "block_n": out.tile_tokens,
+        "num_warps": out.waves_per_workgroup,
+        "num_stages": out.stages,
+        "split": _SPLIT_NAMES[out.split],
+        "partition_size": out.partition_size,
+        "workgroups": out.workgroups,
+    }
+
+
+def _record_launch(args) -> None:
+    cfg = launch_config(args)
+    _last_launch[cfg["path"]] = cfg
+
+
+def _reported(path: str) -> dict | None:
+    cfg = _last_launch.get(path)
+    return None if cfg is None else {k: cfg[k] for k in ("block_n", "num_warps", "num_stages")}
+
+
+def paged_decode_autotune_config() -> dict | None:
+    """Tile configuration of the most recent one-head-per-KV-head launch
+    (triton_ops.py:17-27 reports the Triton autotuner's pick the same way);
+    ``block_n`` = positions per wave loop step, ``num_warps`` = waves per
+    workgroup, ``num_stages`` = tiles in flight per wave. None before any
+    launch of that family."""
+    return _reported("mha_fallback")
+
+
+def paged_decode_grouped_autotune_config() -> dict | None:
+    """As :func:`paged_decode_autotune_config` for the VALU grouped kernel
+    (triton_ops.py:30-40)."""
+    return _reported("scalar_grouped")
+
+
+def paged_decode_grouped_dot_autotune_config() -> dict | None:
+    """As :func:`paged_decode_autotune_config` for the MFMA kernel, the
+    counterpart of the reference's tl.dot grouped kernel (triton_ops.py:43-53)."""
+    return _reported("mfma_grouped")
 
 
 def paged_decode_attention_hip(
@@ -445,14 +499,10 @@ class PreparedPagedAttention:
         self._args.workspace_bytes = ws
         self.partition_size = self._lib.ikl_paged_attention_partition_size(ctypes.byref(self._args))
         a = self._args
-        self.path = _PATH_NAMES[self._lib.ikl_paged_attention_path(
-            a.dtype, a.head_dim, a.block_size, a.table_width, a.num_heads // a.num_kv_heads,
-            a.query_group_size)]
-        # The MFMA family's automatic split is the balanced one whenever it
-        # splits (the library falls back to fixed partitions only for
-        # tables mapping >= 2^29 positions).
-        self.balanced_split = (self.path == "mfma_grouped" and not partition_size and ws > 0
-                               and a.table_width * a.block_size < (1 << 29))
+        self.launch = launch_config(a)
+        self.path = self.launch["path"]
+        self.balanced_split = self.launch["split"] == "balanced"
+        _record_launch(a)
         self.device = query.device
 
     def kernel_names(self) -> tuple[str, str | None]:

@@ -145,3 +145,41 @@ def test_operators_fail_loudly_without_a_gpu():
         ops.append_kv_hip(key, key, cache, torch.zeros(1, dtype=torch.int32))
     assert not ops.hip_available()
     assert ops.triton_available is ops.hip_available
+
+
+@pytest.mark.parametrize(
+    ("dtype", "heads_per_kv", "partition", "expect"),
+    [
+        (_lib.IKL_BF16, 4, 0, ("mfma_grouped", 16, 1, "balanced")),
+        (_lib.IKL_BF16, 4, 512, ("mfma_grouped", 16, 4, "fixed_partitions")),
+        (_lib.IKL_BF16, 4, -1, ("mfma_grouped", 16, 4, "none")),
+        (_lib.IKL_F32, 4, 0, ("scalar_grouped", None, 1, "fixed_partitions")),
+        (_lib.IKL_F16, 1, 0, ("mha_fallback", None, 1, "fixed_partitions")),
+    ],
+)
+def test_launch_config_reports_the_resolved_launch(dtype, heads_per_kv, partition, expect):
+    """ikl_paged_attention_launch_config: the counterpart of the autotune
+    reporters (triton_ops.py:17-53), computed without a launch."""
+    lib = _lib.load()
+    a = _args(dtype=dtype, num_heads=8 * heads_per_kv, num_kv_heads=8, partition_size=partition,
+              max_context_len=8192)
+    out = _lib.LaunchConfig()
+    assert lib.ikl_paged_attention_launch_config(ctypes.byref(a), ctypes.byref(out)) == 0
+    cfg = ops.launch_config(a)
+    path, tile, waves, split = expect
+    assert (cfg["path"], cfg["num_warps"], cfg["split"]) == (path, waves, split)
+    if tile is not None:
+        assert cfg["block_n"] == tile
+    assert 0 < cfg["block_n"] <= 64 and cfg["num_stages"] >= 2 and cfg["workgroups"] > 0
+    if split == "fixed_partitions" and partition > 0:
+        assert cfg["workgroups"] == (8192 // partition) * 8 * a.batch
+    assert lib.ikl_paged_attention_launch_config(ctypes.byref(a), None) == _lib.IKL_EINVAL
+
+
+def test_autotune_reporters_are_none_before_a_launch():
+    import importlib
+
+    fresh = importlib.reload(ops)
+    assert fresh.paged_decode_autotune_config() is None
+    assert fresh.paged_decode_grouped_autotune_config() is None
+    assert fresh.paged_decode_grouped_dot_autotune_config() is None

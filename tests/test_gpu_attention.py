@@ -264,3 +264,95 @@ def test_balanced_and_fixed_partitions_agree():
     assert max_abs_err(a, expected) <= ATOL["bfloat16"]
     assert max_abs_err(b, expected) <= ATOL["bfloat16"]
     assert (a.float() - b.float()).abs().max().item() <= ATOL["bfloat16"]
+
+
+# ------------------------------------------------- the benchmark configurations
+def _fill_by_append(case, ops):
+    """Builds the device cache by appending every context token through the
+    HIP append (slot_mapping slots), then checks it bit for bit against the
+    oracle cache, which holds the same tokens written by index_put."""
+    from inferkernellab_amd.cache import PagedKVCache
+
+    oc = case.oracle_cache
+    cache = PagedKVCache(oc.num_blocks, oc.block_size, oc.num_kv_heads, oc.head_dim,
+                         dtype=getattr(torch, case.dtype), device="cuda")
+    cache.k.zero_()
+    cache.v.zero_()
+    ref = case.device_cache()
+    for b, (table, n) in enumerate(zip(case.tables, case.lengths)):
+        slots = cache.slot_mapping(table, 0, n).to(torch.int32)
+        blocks, offs = (slots // oc.block_size).long(), (slots % oc.block_size).long()
+        ops.append_kv_hip(ref.k[0][blocks, offs].contiguous(), ref.v[0][blocks, offs].contiguous(), cache, slots)
+    torch.cuda.synchronize()
+    for b, (table, n) in enumerate(zip(case.tables, case.lengths)):
+        slots = cache.slot_mapping(table, 0, n)
+        blocks, offs = slots // oc.block_size, slots % oc.block_size
+        got = cache.k[0][blocks, offs]
+        want = ref.k[0][blocks, offs]
+        assert torch.equal(got.view(torch.int16) if got.element_size() == 2 else got.view(torch.int32),
+                           want.view(torch.int16) if want.element_size() == 2 else want.view(torch.int32))
+    return cache
+
+
+def test_config_gqa_fp32_hd64_b4_ctx512():
+    """GQA 32/8, head_dim 64, fp32, batch 4 x 512, block 16, 159-block pool,
+    scale 1/8; the cache filled by appending every context token."""
+    from inferkernellab_amd import ops
+
+    case = make_case(batch=4, num_heads=32, num_kv_heads=8, head_dim=64, block_size=16,
+                     lengths=[512] * 4, dtype="float32", seed=0, num_blocks=159)
+    cache = _fill_by_append(case, ops)
+    out = ops.paged_decode_attention_hip(case.device_query(), cache, case.device_tables(), case.device_lengths(),
+                                         scale=0.125)
+    torch.cuda.synchronize()
+    assert max_abs_err(out, case.expected(scale=0.125)) <= ATOL["float32"]
+
+
+def test_config_mha_fp16_hd128_b16_ctx512_with_append_step():
+    """MHA 32/32, head_dim 128, fp16, batch 16: 511 cached tokens, one
+    appended per request through slot_mapping, then attention over 512;
+    pool batch * ceil(512/16) + 8 = 520 blocks."""
+    from inferkernellab_amd import ops
+
+    case = make_case(batch=16, num_heads=32, num_kv_heads=32, head_dim=128, block_size=16,
+                     lengths=[512] * 16, dtype="float16", seed=2, num_blocks=520)
+    cache = case.device_cache()
+    # rewrite token 511 of every request through the HIP append (the step's append)
+    slots = torch.cat([cache.slot_mapping(t, 511, 1) for t in case.tables]).to(torch.int32)
+    blocks, offs = (slots // 16).long(), (slots % 16).long()
+    new_k, new_v = cache.k[0][blocks, offs].clone(), cache.v[0][blocks, offs].clone()
+    cache.k[0][blocks, offs] = 0
+    cache.v[0][blocks, offs] = 0
+    ops.append_kv_hip(new_k, new_v, cache, slots)
+    out = ops.paged_decode_attention_hip(case.device_query(), cache, case.device_tables(), case.device_lengths())
+    torch.cuda.synchronize()
+    assert torch.equal(cache.k[0][blocks, offs].view(torch.int16), new_k.view(torch.int16))
+    assert max_abs_err(out, case.expected()) <= ATOL["float16"]
+
+
+def test_config_mqa_bf16_hd128_b64_ctx1k_4k():
+    """MQA 32/1, head_dim 128, bf16, batch 64, contexts U[1024, 4096], K/V
+    0.5 * N(0, 1), scattered tables: one 32-head group per K/V tile."""
+    gen = np.random.default_rng(3)
+    lengths = [int(x) for x in gen.integers(1024, 4097, size=64)]
+    case = make_case(batch=64, num_heads=32, num_kv_heads=1, head_dim=128, block_size=16,
+                     lengths=lengths, dtype="bfloat16", seed=3, kv_scale=0.5)
+    _check(case, "paged_decode_attention_hip", label="mqa-b64")
+    _check(case, "paged_decode_attention_hip_grouped", label="mqa-b64-grouped", query_group_size=8)
+
+
+def test_autotune_reporters_describe_the_last_launch():
+    from inferkernellab_amd import ops
+
+    case = make_case(batch=2, num_heads=8, num_kv_heads=2, head_dim=128, block_size=16,
+                     lengths=[300, 40], dtype="bfloat16", seed=50)
+    ops.paged_decode_attention_hip(case.device_query(), case.device_cache(), case.device_tables(),
+                                   case.device_lengths())
+    cfg = ops.paged_decode_grouped_dot_autotune_config()
+    assert cfg == {"block_n": 16, "num_warps": 1, "num_stages": 2}
+    case32 = make_case(batch=2, num_heads=8, num_kv_heads=8, head_dim=64, block_size=16,
+                       lengths=[30, 40], dtype="float32", seed=51)
+    ops.paged_decode_attention_hip(case32.device_query(), case32.device_cache(), case32.device_tables(),
+                                   case32.device_lengths())
+    mha = ops.paged_decode_autotune_config()
+    assert set(mha) == {"block_n", "num_warps", "num_stages"} and mha["num_warps"] == 1
