@@ -356,3 +356,23 @@ def test_autotune_reporters_describe_the_last_launch():
                                    case32.device_lengths())
     mha = ops.paged_decode_autotune_config()
     assert set(mha) == {"block_n", "num_warps", "num_stages"} and mha["num_warps"] == 1
+
+
+@pytest.mark.parametrize("lengths,heads,kv", [([4096, 17, 8192, 5000, 1, 6000, 333, 7777], 32, 8),
+                                             ([20000], 8, 1)])
+def test_prepared_balanced_split_repeats_bit_identically(lengths, heads, kv):
+    """One prepared workspace serves repeated balanced-split launches (a unit
+    over ~1250 waves included) with bit-identical results."""
+    from inferkernellab_amd import ops
+
+    case = make_case(batch=len(lengths), num_heads=heads, num_kv_heads=kv, head_dim=128, block_size=16,
+                     lengths=lengths, dtype="bfloat16", seed=47)
+    attn = ops.PreparedPagedAttention(case.device_query(), case.device_cache(), case.device_tables(),
+                                      case.device_lengths(), max_context_len=max(lengths))
+    assert attn.balanced_split
+    first = attn().clone()
+    for _ in range(4):
+        again = attn()
+        torch.cuda.synchronize()
+        assert torch.equal(again.view(torch.int16), first.view(torch.int16))
+    assert max_abs_err(first, case.expected()) <= ATOL["bfloat16"]
