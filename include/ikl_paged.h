@@ -133,6 +133,47 @@ typedef struct ikl_paged_attention_args {
   void *events[3];
 } ikl_paged_attention_args;
 
+/* Arguments of ikl_rope_append_kv: rotary embedding of q and k fused with
+ * the KV append. Replaces the step of hf_benchmark.py:419-436 (rotate-half
+ * RoPE of hf_benchmark.py:69-85, then _write_kv -> append_kv_triton /
+ * cache.write): one launch instead of the elementwise RoPE ops plus the
+ * append. */
+typedef struct ikl_rope_append_args {
+  const void *query;         /* [num_tokens, num_heads, head_dim]; NULL when num_heads == 0 */
+  int64_t q_stride_t, q_stride_h;
+  void *query_out;           /* rotated query (may be `query`) */
+  int64_t q_out_stride_t, q_out_stride_h;
+  const void *key;           /* [num_tokens, num_kv_heads, head_dim], before rotation */
+  int64_t key_stride_t, key_stride_h;
+  const void *value;         /* [num_tokens, num_kv_heads, head_dim] */
+  int64_t value_stride_t, value_stride_h;
+  const void *cos;           /* [num_tokens, head_dim] of each token's position, tensor dtype */
+  int64_t cos_stride_t;
+  const void *sin;           /* [num_tokens, head_dim] */
+  int64_t sin_stride_t;
+  const void *slots;         /* [num_tokens] physical slot per token */
+  int32_t slot_type;         /* enum ikl_index_type */
+  void *k_cache;             /* base of cache.k[layer] */
+  void *v_cache;             /* base of cache.v[layer] */
+  int64_t k_stride_block, k_stride_token, k_stride_head;
+  int64_t v_stride_block, v_stride_token, v_stride_head;
+  int64_t num_tokens;
+  int64_t num_blocks;
+  int32_t block_size;
+  int32_t num_heads;         /* 0: rotate and append keys only */
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t dtype;             /* enum ikl_dtype of every tensor */
+} ikl_rope_append_args;
+
+/* Rotary embedding + KV append in one launch: query_out = rope(query);
+ * cache.k[slot] = rope(key); cache.v[slot] = value; rope(x) = x * cos +
+ * rotate_half(x) * sin with rotate_half(x) = [-x2, x1]. Bit-exact with the
+ * torch elementwise sequence on the same cos / sin rows (each product and
+ * the sum rounded to the tensor dtype). Slots outside the cache are
+ * skipped; query rows are rotated regardless. */
+int ikl_rope_append_kv(const ikl_rope_append_args *args, void *stream);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char *ikl_last_error(void);
 

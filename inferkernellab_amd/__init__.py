@@ -21,6 +21,7 @@ from .ops import (
     paged_decode_grouped_autotune_config,
     paged_decode_grouped_dot_autotune_config,
     paged_decode_grouped_path,
+    rope_append_kv_hip,
     triton_append_available,
     triton_available,
 )
@@ -45,6 +46,7 @@ __all__ = [
     "paged_decode_attention_triton",
     "paged_decode_attention_triton_grouped",
     "paged_decode_grouped_path",
+    "rope_append_kv_hip",
     "paged_decode_autotune_config",
     "paged_decode_grouped_autotune_config",
     "paged_decode_grouped_dot_autotune_config",

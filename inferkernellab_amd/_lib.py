@@ -32,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "ikl_paged_attention",
     "ikl_paged_attention_path",
     "ikl_paged_attention_launch_config",
+    "ikl_rope_append_kv",
 )
 
 _c_i64 = ctypes.c_int64
@@ -110,6 +111,46 @@ class PagedAttentionArgs(ctypes.Structure):
     ]
 
 
+class RopeAppendArgs(ctypes.Structure):
+    """Mirror of ikl_rope_append_args."""
+
+    _fields_ = [
+        ("query", _c_ptr),
+        ("q_stride_t", _c_i64),
+        ("q_stride_h", _c_i64),
+        ("query_out", _c_ptr),
+        ("q_out_stride_t", _c_i64),
+        ("q_out_stride_h", _c_i64),
+        ("key", _c_ptr),
+        ("key_stride_t", _c_i64),
+        ("key_stride_h", _c_i64),
+        ("value", _c_ptr),
+        ("value_stride_t", _c_i64),
+        ("value_stride_h", _c_i64),
+        ("cos", _c_ptr),
+        ("cos_stride_t", _c_i64),
+        ("sin", _c_ptr),
+        ("sin_stride_t", _c_i64),
+        ("slots", _c_ptr),
+        ("slot_type", _c_i32),
+        ("k_cache", _c_ptr),
+        ("v_cache", _c_ptr),
+        ("k_stride_block", _c_i64),
+        ("k_stride_token", _c_i64),
+        ("k_stride_head", _c_i64),
+        ("v_stride_block", _c_i64),
+        ("v_stride_token", _c_i64),
+        ("v_stride_head", _c_i64),
+        ("num_tokens", _c_i64),
+        ("num_blocks", _c_i64),
+        ("block_size", _c_i32),
+        ("num_heads", _c_i32),
+        ("num_kv_heads", _c_i32),
+        ("head_dim", _c_i32),
+        ("dtype", _c_i32),
+    ]
+
+
 class LaunchConfig(ctypes.Structure):
     """Mirror of ikl_launch_config."""
 
@@ -144,6 +185,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ikl_paged_attention.argtypes = [ctypes.POINTER(PagedAttentionArgs), _c_ptr]
     lib.ikl_paged_attention_path.restype = _c_i32
     lib.ikl_paged_attention_path.argtypes = [_c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32]
+    lib.ikl_rope_append_kv.restype = ctypes.c_int
+    lib.ikl_rope_append_kv.argtypes = [ctypes.POINTER(RopeAppendArgs), _c_ptr]
     lib.ikl_paged_attention_launch_config.restype = ctypes.c_int
     lib.ikl_paged_attention_launch_config.argtypes = [ctypes.POINTER(PagedAttentionArgs),
                                                       ctypes.POINTER(LaunchConfig)]

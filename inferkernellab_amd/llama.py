@@ -2,10 +2,12 @@
 
 ``LlamaPagedDecodeRunner`` is the caller of the paged path for a Llama
 model (hf_benchmark.py:131-700). Per decode step and layer it computes
-q/k/v for one token per request, rotates q and k (rotate-half RoPE), writes
-k/v into the paged cache with the HIP append, runs the HIP paged decode
-attention over the request's whole context (the current token included) and
-finishes the layer (o_proj + residual, SwiGLU MLP + residual). Batched
+q/k/v for one token per request, rotates q and k (rotate-half RoPE) and
+writes the rotated k and v into the paged cache in one fused HIP launch
+(ikl_rope_append_kv; with ``append_backend="torch"``: torch RoPE and the
+cache's index_put), runs the HIP paged decode attention over the request's
+whole context (the current token included) and finishes the layer (o_proj +
+residual, SwiGLU MLP + residual). Batched
 prefill writes a whole prompt chunk per request, then attends causally over
 the gathered paged prefix.
 
@@ -290,13 +292,20 @@ class LlamaPagedDecodeRunner:
         cos, sin = m.rotary_emb(hidden.unsqueeze(1), pos)  # [n, 1, D]: broadcasts over heads
         tables, lens = self.metadata.for_batch(requests, [p + 1 for p in positions])
         slots = self.metadata.slots(requests, positions, self.cache.layout.block_size)
+        fused = self.append_backend != "torch"
+        if fused:
+            cos2, sin2 = cos.reshape(n, self.head_dim).contiguous(), sin.reshape(n, self.head_dim).contiguous()
         for li, layer in enumerate(m.layers):
             x = layer.input_layernorm(hidden)
             att = layer.self_attn
-            q = self._rope(att.q_proj(x).view(n, self.num_heads, self.head_dim), cos, sin)
-            k = self._rope(att.k_proj(x).view(n, self.num_kv_heads, self.head_dim), cos, sin)
+            q = att.q_proj(x).view(n, self.num_heads, self.head_dim)
+            k = att.k_proj(x).view(n, self.num_kv_heads, self.head_dim)
             v = att.v_proj(x).view(n, self.num_kv_heads, self.head_dim)
-            self._append(li, slots, k, v)
+            if fused:  # RoPE of q and k + append of rope(k), v: one launch (q rotated in place)
+                ops.rope_append_kv_hip(q, k, v, cos2, sin2, self.cache, slots, layer=li)
+            else:
+                q, k = self._rope(q, cos, sin), self._rope(k, cos, sin)
+                self._append(li, slots, k, v)
             o = self._attend(q.contiguous(), self.cache, tables, lens, layer=li, validate_inputs=(li == 0))
             hidden = hidden + att.o_proj(o.reshape(n, self.num_heads * self.head_dim))
             hidden = self._mlp_residual(layer, hidden)

@@ -438,6 +438,74 @@ def append_kv_hip(key: torch.Tensor, value: torch.Tensor, cache, slots: torch.Te
     _lib.check(status, "append_kv")
 
 
+def rope_append_kv_hip(query: torch.Tensor | None, key: torch.Tensor, value: torch.Tensor,
+                       cos: torch.Tensor, sin: torch.Tensor, cache, slots: torch.Tensor, layer: int = 0,
+                       *, query_out: torch.Tensor | None = None) -> torch.Tensor | None:
+    """Rotary embedding of q and k fused with the KV append (one launch).
+
+    ``query`` ``[T, H, D]`` (or None), ``key`` / ``value`` ``[T, Hkv, D]``,
+    ``cos`` / ``sin`` ``[T, D]`` rows of each token's position in the tensors'
+    dtype, ``slots`` ``[T]``. Writes ``rope(key)`` and ``value`` into
+    ``cache.k[layer]`` / ``cache.v[layer]`` at the slots and returns
+    ``rope(query)`` (into ``query_out``, default: ``query`` in place).
+    ``rope(x) = x * cos + rotate_half(x) * sin`` as hf_benchmark.py:69-85,
+    bit-exact with the torch elementwise ops on the same rows. Slots outside
+    the cache are skipped.
+    """
+    lib = _require_backend()
+    layout = cache.layout
+    if key.shape != value.shape or key.ndim != 3 or tuple(key.shape[1:]) != (layout.num_kv_heads, layout.head_dim):
+        raise ValueError("key/value must have shape [T, Hkv, D] matching the cache layout")
+    t = key.shape[0]
+    if cos.shape != (t, layout.head_dim) or sin.shape != cos.shape:
+        raise ValueError("cos/sin must have shape [T, head_dim]")
+    if query is not None and (query.ndim != 3 or query.shape[0] != t or query.shape[2] != layout.head_dim
+                              or query.shape[1] % layout.num_kv_heads != 0):
+        raise ValueError("query must have shape [T, H, head_dim] with H a multiple of num_kv_heads")
+    tensors = [key, value, cos, sin] + ([query] if query is not None else [])
+    if any(x.dtype != cache.dtype for x in tensors):
+        raise ValueError("query/key/value/cos/sin must share the cache dtype")
+    if any(x.device != cache.device for x in tensors) or slots.device != cache.device:
+        raise ValueError("tensors must be on the cache device")
+    if slots.dtype not in _INDEX_TYPES or slots.numel() != t:
+        raise ValueError("slots must be int32/int64 with one entry per token")
+    if not 0 <= layer < layout.num_layers:
+        raise IndexError("layer is out of range")
+    key, value, cos, sin = (x if _aligned_rows(x) else x.contiguous() for x in (key, value, cos, sin))
+    if query is not None:
+        if not _aligned_rows(query):
+            query = query.contiguous()
+        if query_out is None:
+            query_out = query
+        elif query_out.shape != query.shape or query_out.dtype != query.dtype or not _aligned_rows(query_out):
+            raise ValueError("query_out must match query and have 16-byte aligned rows")
+    slots = slots.reshape(-1).contiguous()
+    if t == 0:
+        return query_out
+    a = _lib.RopeAppendArgs()
+    if query is not None:
+        a.query, a.q_stride_t, a.q_stride_h = query.data_ptr(), query.stride(0), query.stride(1)
+        a.query_out, a.q_out_stride_t, a.q_out_stride_h = query_out.data_ptr(), query_out.stride(0), query_out.stride(1)
+        a.num_heads = query.shape[1]
+    a.key, a.key_stride_t, a.key_stride_h = key.data_ptr(), key.stride(0), key.stride(1)
+    a.value, a.value_stride_t, a.value_stride_h = value.data_ptr(), value.stride(0), value.stride(1)
+    a.cos, a.cos_stride_t = cos.data_ptr(), cos.stride(0)
+    a.sin, a.sin_stride_t = sin.data_ptr(), sin.stride(0)
+    a.slots = slots.data_ptr()
+    a.slot_type = _INDEX_TYPES[slots.dtype]
+    kc, vc = cache.k[layer], cache.v[layer]
+    a.k_cache, a.v_cache = kc.data_ptr(), vc.data_ptr()
+    a.k_stride_block, a.k_stride_token, a.k_stride_head = kc.stride(0), kc.stride(1), kc.stride(2)
+    a.v_stride_block, a.v_stride_token, a.v_stride_head = vc.stride(0), vc.stride(1), vc.stride(2)
+    a.num_tokens, a.num_blocks, a.block_size = t, layout.num_blocks, layout.block_size
+    a.num_kv_heads, a.head_dim, a.dtype = layout.num_kv_heads, layout.head_dim, _DTYPES[cache.dtype]
+    with torch.cuda.device(key.device):
+        stream = torch.cuda.current_stream(key.device).cuda_stream
+        status = lib.ikl_rope_append_kv(ctypes.byref(a), ctypes.c_void_p(stream))
+    _lib.check(status, "rope_append_kv")
+    return query_out
+
+
 def _append_args(key, value, cache, slots, layer):
     layout = cache.layout
     k_cache = cache.k[layer]

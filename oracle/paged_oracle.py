@@ -14,6 +14,7 @@ It restates, in numpy, the reference's algorithm for this path:
 * ``expand_kv``                  — attention.py:9-15 (repeat_interleave)
 * ``dense_decode_attention``     — attention.py:18-36 (fp32 einsum/softmax/einsum)
 * ``paged_decode_attention``     — attention.py:134-175 (= backend ``paged_reference``)
+* ``rope_rows``                  — hf_benchmark.py:69-85 (rotate-half RoPE before the append)
 
 Storage keeps the cache's own element type: float16 and float32 as numpy
 arrays of that type, bfloat16 as raw ``uint16`` bit patterns (numpy has no
@@ -29,7 +30,9 @@ Parity pins (each checked in tests/test_oracle.py):
 * attention: float64 brute force on tiny inputs, closed forms (context 1 ->
   v, equal keys -> mean of v, one dominant key -> its v), MHA == GQA after
   explicit head expansion, block-table permutation invariance, and torch's
-  own softmax/einsum on the same data.
+  own softmax/einsum on the same data;
+* rope_rows: torch's own elementwise ops on the same storage, bit for bit,
+  in the three dtypes; position 0 (cos 1, sin 0) is the identity.
 """
 
 from __future__ import annotations
@@ -70,6 +73,22 @@ def cast_output(x: np.ndarray, dtype: str) -> np.ndarray:
     if dtype == "bfloat16":
         return f32_to_bf16_bits(x)
     return np.asarray(x, dtype=np.float32).astype(storage_dtype(dtype))
+
+
+# ------------------------------------------------------------------- rope
+def rope_rows(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, dtype: str) -> np.ndarray:
+    """Rotate-half RoPE on storage arrays, with the rounding of the
+    reference's torch ops (hf_benchmark.py:69-85): ``x * cos`` and
+    ``rotate_half(x) * sin`` each rounded to ``dtype``, then their sum
+    rounded. x ``[..., D]``; cos / sin broadcast against x. Returns storage."""
+    half = x.shape[-1] // 2
+    xf, cf, sf = to_f32(x, dtype), to_f32(cos, dtype), to_f32(sin, dtype)
+    rot = np.concatenate([-xf[..., half:], xf[..., :half]], axis=-1)
+
+    def rnd(v):  # one elementwise op's result in `dtype`
+        return to_f32(cast_output(v, dtype), dtype)
+
+    return cast_output(rnd(xf * cf) + rnd(rot * sf), dtype)
 
 
 # -------------------------------------------------------------------- cache

@@ -34,7 +34,9 @@ def test_library_exports_every_declared_symbol():
 def test_struct_layouts_match_header_field_order():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     for struct_name, cls in (("ikl_append_args", _lib.AppendArgs),
-                             ("ikl_paged_attention_args", _lib.PagedAttentionArgs)):
+                             ("ikl_paged_attention_args", _lib.PagedAttentionArgs),
+                             ("ikl_rope_append_args", _lib.RopeAppendArgs),
+                             ("ikl_launch_config", _lib.LaunchConfig)):
         body = re.search(r"typedef struct %s \{(.*?)\}" % struct_name, text, flags=re.S).group(1)
         fields = []
         for decl in body.split(";"):
@@ -183,3 +185,17 @@ def test_autotune_reporters_are_none_before_a_launch():
     assert fresh.paged_decode_autotune_config() is None
     assert fresh.paged_decode_grouped_autotune_config() is None
     assert fresh.paged_decode_grouped_dot_autotune_config() is None
+
+
+def test_rope_append_rejects_bad_arguments_without_a_gpu():
+    """ikl_rope_append_kv validates before launching: errors, not launches."""
+    lib = _lib.load()
+    a = _lib.RopeAppendArgs()
+    assert lib.ikl_rope_append_kv(None, None) == _lib.IKL_EINVAL
+    a.num_tokens = 4
+    assert lib.ikl_rope_append_kv(ctypes.byref(a), None) == _lib.IKL_EINVAL  # zero dims
+    a.num_blocks, a.block_size, a.num_kv_heads, a.head_dim, a.dtype = 8, 16, 2, 128, _lib.IKL_BF16
+    assert lib.ikl_rope_append_kv(ctypes.byref(a), None) == _lib.IKL_EINVAL
+    assert "null tensor" in _lib.last_error()
+    a.num_tokens = 0
+    assert lib.ikl_rope_append_kv(ctypes.byref(a), None) == _lib.IKL_OK  # nothing to do

@@ -237,3 +237,45 @@ def test_bench_bytes_formula_matches_reference_kv_term():
     assert kv == 8388608  # the 8.4 MB of the CPU fp32 batch-4 workload
     assert total == kv + 2 * b * 32 * d * eb + b * (ctx // 16) * 4 + b * 4
     assert math.isclose(total / kv, 1.0, rel_tol=0.01)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16", "float32"])
+def test_rope_rows_match_torch_ops_bit_for_bit(dtype):
+    """rope_rows against torch's elementwise sequence of hf_benchmark.py:69-85
+    (x * cos + rotate_half(x) * sin in the tensor dtype)."""
+    gen = torch.Generator().manual_seed(11)
+    tdt = getattr(torch, dtype)
+    x = torch.randn(7, 4, 64, generator=gen).to(tdt)
+    ang = torch.rand(7, 32, generator=gen) * 50
+    emb = torch.cat([ang, ang], dim=-1)
+    cos, sin = emb.cos().to(tdt), emb.sin().to(tdt)
+
+    def rot(v):
+        return torch.cat((-v[..., 32:], v[..., :32]), dim=-1)
+
+    want = x * cos[:, None, :] + rot(x) * sin[:, None, :]
+
+    def storage(t):
+        return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
+
+    got = po.rope_rows(storage(x), storage(cos)[:, None, :], storage(sin)[:, None, :], dtype)
+    assert np.array_equal(got.view(np.uint8), storage(want).view(np.uint8))
+    ones, zeros = torch.ones(7, 64).to(tdt), torch.zeros(7, 64).to(tdt)
+    ident = po.rope_rows(storage(x), storage(ones)[:, None, :], storage(zeros)[:, None, :], dtype)
+    assert np.array_equal(ident.view(np.uint8), storage(x).view(np.uint8))
+
+
+def test_planted_rope_sign_mistake_is_caught(monkeypatch):
+    gen = torch.Generator().manual_seed(12)
+    x = torch.randn(3, 2, 16, generator=gen)
+    emb = torch.rand(3, 16, generator=gen)
+    cos, sin = emb.cos(), emb.sin()
+    want = x * cos[:, None] + torch.cat((-x[..., 8:], x[..., :8]), -1) * sin[:, None]
+    real = po.rope_rows
+
+    def wrong(xs, c, s, dtype):  # the sin term's sign flipped
+        return real(xs, c, -s, dtype)
+
+    monkeypatch.setattr(po, "rope_rows", wrong)
+    got = po.rope_rows(x.numpy(), cos.numpy()[:, None], sin.numpy()[:, None], "float32")
+    assert np.abs(got - want.numpy()).max() > 1e-3
