@@ -151,6 +151,20 @@ def random_llama(config: LlamaConfig, *, seed: int = 0, device="cuda",
 
 
 # --------------------------------------------------------------- the runner
+@dataclass
+class _StepBuffers:
+    """Static device buffers of one captured decode step."""
+
+    ids: torch.Tensor
+    logits: torch.Tensor
+    pos: torch.Tensor
+    tok: torch.Tensor
+    lens: torch.Tensor
+    slots: torch.Tensor
+    used: torch.Tensor | None = None
+    graph: torch.cuda.CUDAGraph | None = None
+
+
 @dataclass(frozen=True)
 class LlamaPagedRunResult:
     """Outcome and timing of a Llama run (fields of hf_benchmark.py:88-128)."""
@@ -203,7 +217,7 @@ class LlamaPagedDecodeRunner:
                  backend: str = "hip_paged_grouped", block_size: int = 16, append_backend: str = "hip",
                  max_num_batched_tokens: int = 2048, prefill_mode: str = "batched",
                  temperature: float = 0.0, top_p: float = 1.0, seed: int = 2026,
-                 eos_token_ids: Sequence[int] | None = None) -> None:
+                 eos_token_ids: Sequence[int] | None = None, use_graph: bool = True) -> None:
         if not prompts:
             raise ValueError("at least one prompt is required")
         if max_new_tokens <= 0:
@@ -266,6 +280,9 @@ class LlamaPagedDecodeRunner:
         self._finish = {r.request_id: "length" for r in self.requests}
         self._generators = {r.request_id: torch.Generator(device=self.device).manual_seed(seed + r.request_id)
                             for r in self.requests}
+        self.use_graph = use_graph
+        self._graphs: dict[tuple[int, ...], _StepBuffers] = {}
+        self._max_ctx = max(self.prompt_lengths) + max_new_tokens
         self._has_run = False
 
     # ------------------------------------------------------------ helpers
@@ -285,13 +302,20 @@ class LlamaPagedDecodeRunner:
     # ------------------------------------------------------- decode forward
     def _forward_decode(self, token_ids: torch.Tensor, requests, positions) -> torch.Tensor:
         """Logits [B, vocab] after one token per request at `positions`."""
-        m = self.model.model
-        n = len(requests)
-        hidden = m.embed_tokens(token_ids.to(device=self.device, dtype=torch.long))
-        pos = torch.tensor(list(positions), dtype=torch.long, device=self.device).view(n, 1)
-        cos, sin = m.rotary_emb(hidden.unsqueeze(1), pos)  # [n, 1, D]: broadcasts over heads
+        pos = torch.tensor(list(positions), dtype=torch.long, device=self.device)
         tables, lens = self.metadata.for_batch(requests, [p + 1 for p in positions])
         slots = self.metadata.slots(requests, positions, self.cache.layout.block_size)
+        return self._decode_layers(token_ids.to(device=self.device, dtype=torch.long), pos, tables, lens, slots,
+                                   validate=True)
+
+    def _decode_layers(self, token_ids, pos, tables, lens, slots, *, validate: bool) -> torch.Tensor:
+        """The decode forward on device metadata: token_ids / pos [n] long,
+        tables [n, W] int32, lens / slots [n] int32 (no host synchronisation
+        unless `validate`, so it can be captured in a graph)."""
+        m = self.model.model
+        n = token_ids.shape[0]
+        hidden = m.embed_tokens(token_ids)
+        cos, sin = m.rotary_emb(hidden.unsqueeze(1), pos.view(n, 1))  # [n, 1, D]: broadcasts over heads
         fused = self.append_backend != "torch"
         if fused:
             cos2, sin2 = cos.reshape(n, self.head_dim).contiguous(), sin.reshape(n, self.head_dim).contiguous()
@@ -306,7 +330,8 @@ class LlamaPagedDecodeRunner:
             else:
                 q, k = self._rope(q, cos, sin), self._rope(k, cos, sin)
                 self._append(li, slots, k, v)
-            o = self._attend(q.contiguous(), self.cache, tables, lens, layer=li, validate_inputs=(li == 0))
+            o = self._attend(q.contiguous(), self.cache, tables, lens, layer=li, validate_inputs=validate and li == 0,
+                             max_context_len=self._max_ctx)
             hidden = hidden + att.o_proj(o.reshape(n, self.num_heads * self.head_dim))
             hidden = self._mlp_residual(layer, hidden)
         return self.model.lm_head(m.norm(hidden))
@@ -402,7 +427,67 @@ class LlamaPagedDecodeRunner:
             tok = torch.multinomial(logp.exp(), 1, generator=gen).squeeze(-1)
         return tok, policy[tok], logp[tok]
 
+    # ------------------------------------------------- graph-captured steps
+    def _decode_graphed(self, requests: tuple[InferenceRequest, ...]) -> None:
+        """Greedy decode step as one HIP graph replay per batch composition.
+
+        The graph holds the whole step on static device buffers: argmax of
+        the previous logits, lens = pos + 1 and slots from the table buffer
+        on the device, the layers (fused RoPE + append, paged attention),
+        lm_head, and pos += 1. The host only publishes new table entries and
+        reads the tokens back. A batch's first step runs eagerly (it is that
+        step's execution) and is then captured."""
+        key = tuple(r.request_id for r in requests)
+        self.metadata.sync_tables(requests)
+        st = self._graphs.get(key)
+        if st is None:
+            n = len(requests)
+            st = _StepBuffers(
+                ids=torch.tensor(key, dtype=torch.long, device=self.device),
+                logits=torch.stack([self._next_logits[r.request_id] for r in requests]).contiguous(),
+                pos=torch.tensor([r.prompt_tokens + r.generated_tokens for r in requests], dtype=torch.long,
+                                 device=self.device),
+                tok=torch.zeros(n, dtype=torch.long, device=self.device),
+                lens=torch.zeros(n, dtype=torch.int32, device=self.device),
+                slots=torch.zeros(n, dtype=torch.int32, device=self.device),
+            )
+            st.used = torch.empty_like(st.logits)
+            side = torch.cuda.Stream(self.device)
+            side.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(side):
+                self._graph_body(st)  # this step's execution
+            torch.cuda.current_stream(self.device).wait_stream(side)
+            st.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(st.graph):
+                self._graph_body(st)
+            self._graphs[key] = st
+        else:
+            st.graph.replay()
+        self._decode_logits.append(st.used.float().cpu())
+        toks = st.tok.tolist()
+        for i, r in enumerate(requests):
+            self._generated[r.request_id].append(int(toks[i]))
+            self._next_logits[r.request_id] = st.logits[i]
+
+    def _graph_body(self, st: "_StepBuffers") -> None:
+        bs = self.cache.layout.block_size
+        st.used.copy_(st.logits)
+        st.tok.copy_(st.used.argmax(dim=-1))
+        st.lens.copy_(st.pos + 1)
+        tables = self.metadata.tables.index_select(0, st.ids)
+        # The runtime reserves every decoded position inside the table's
+        # width; the clamp keeps a stray replay (positions past the run) from
+        # indexing outside the table buffer.
+        col = (st.pos // bs).clamp(max=self.metadata.width - 1)
+        blocks = tables.gather(1, col.view(-1, 1)).view(-1).to(torch.long)
+        st.slots.copy_(blocks * bs + st.pos % bs)
+        st.logits.copy_(self._decode_layers(st.tok, st.pos, tables, st.lens, st.slots, validate=False))
+        st.pos.add_(1)
+
     def _decode(self, requests: tuple[InferenceRequest, ...]) -> None:
+        if self.use_graph and self.temperature == 0 and not self.eos_token_ids:
+            self._decode_graphed(requests)
+            return
         used = torch.stack([self._next_logits[r.request_id] for r in requests])
         sampled = None
         if self.temperature == 0 and not self.eos_token_ids:

@@ -321,3 +321,20 @@ def test_llama_e2e_bf16_matches_same_dtype_eager():
     print(f"bf16 e2e vs same-dtype eager: logits max err {worst:.4f} (prompt logits {worst0:.4f}), "
           f"greedy agreement {matched}/{total}", flush=True)
     assert worst <= bound and matched >= 0.95 * total
+
+
+def test_llama_graph_decode_equals_eager_decode():
+    """use_graph (the greedy step replayed as one HIP graph) gives the eager
+    step's logits and tokens bit for bit."""
+    from inferkernellab_amd.llama import LlamaPagedDecodeRunner
+
+    cfg, model = _llama(torch.bfloat16, hidden_size=512, intermediate_size=1024, num_attention_heads=8,
+                        num_key_value_heads=2, vocab_size=256, head_dim=64)
+    gen = np.random.default_rng(9)
+    prompts = [gen.integers(0, 256, size=n).tolist() for n in (40, 17, 95)]
+    runs = [LlamaPagedDecodeRunner(model, prompts, max_new_tokens=20, block_size=16, use_graph=g).run()
+            for g in (True, False)]
+    assert runs[0].generated_tokens == runs[1].generated_tokens
+    for a, b in zip(runs[0].decode_logits, runs[1].decode_logits):
+        assert torch.equal(a, b)
+    assert runs[0].cache_released
