@@ -174,6 +174,57 @@ typedef struct ikl_rope_append_args {
  * skipped; query rows are rotated regardless. */
 int ikl_rope_append_kv(const ikl_rope_append_args *args, void *stream);
 
+/* Arguments of ikl_paged_prefill_attention.
+ * Replaces paged_prefill_attention_sdpa (attention.py:230-321, called by the
+ * batched prefill at hf_benchmark.py:491-498): the gather of the whole
+ * prefix into dense K/V plus a masked SDPA, per layer. */
+typedef struct ikl_paged_prefill_args {
+  const void *query;         /* [batch, num_heads, query_width, head_dim] */
+  int64_t q_stride_b, q_stride_h, q_stride_t;
+  const void *k_cache;       /* base of cache.k[layer] */
+  const void *v_cache;       /* base of cache.v[layer] */
+  int64_t k_stride_block, k_stride_token, k_stride_head;
+  int64_t v_stride_block, v_stride_token, v_stride_head;
+  const void *block_tables;  /* [batch, table_width] physical block ids */
+  int32_t table_type;        /* enum ikl_index_type */
+  int64_t table_stride_b;
+  int64_t table_width;
+  const void *query_starts;  /* [batch] position of query row 0 */
+  const void *context_lens;  /* [batch] end of the prefill range (exclusive) */
+  int32_t lens_type;         /* enum ikl_index_type of query_starts and context_lens */
+  void *out;                 /* [batch, num_heads, query_width, head_dim], dtype of query */
+  int64_t out_stride_b, out_stride_h, out_stride_t;
+  int64_t batch;
+  int64_t query_width;
+  int64_t num_blocks;
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t block_size;
+  int32_t dtype;             /* enum ikl_dtype (query, cache and out share it) */
+  float scale;               /* softmax scale; <= 0 selects head_dim**-0.5 */
+  /* Kernel family: -1 = automatic (ikl_paged_prefill_path), else
+   * IKL_PATH_MFMA_GROUPED or IKL_PATH_SCALAR_GROUPED. */
+  int32_t path;
+  /* Optional hipEvent_t handles recorded on `stream` before [0] and after
+   * [1] the attention kernel. NULL entries are skipped. */
+  void *events[2];
+} ikl_paged_prefill_args;
+
+/* Causal prefill attention over the paged cache. Row t of request b sits at
+ * position query_starts[b] + t; rows t < context_lens[b] - query_starts[b]
+ * attend the positions <= their own, the other rows of the query width
+ * receive the value at position 0 (what the reference's mask leaves them).
+ * The cache must already hold positions [0, context_lens[b]). Positions
+ * whose block id is outside [0, num_blocks) are masked; the kernels never
+ * read outside the cache. Replaces attention.py:230-321. */
+int ikl_paged_prefill_attention(const ikl_paged_prefill_args *args, void *stream);
+
+/* Kernel family a prefill launch uses: IKL_PATH_MFMA_GROUPED for fp16/bf16
+ * with head_dim in {32, 64, 96, 128} and block_size a multiple of 16, else
+ * IKL_PATH_SCALAR_GROUPED. dtype: enum ikl_dtype. */
+int32_t ikl_paged_prefill_path(int32_t dtype, int32_t head_dim, int32_t block_size);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char *ikl_last_error(void);
 

@@ -1,10 +1,10 @@
 """MI355X (gfx950) paged-KV decode path for InferKernelLab.
 
-Hand-written HIP kernels (KV append, paged decode attention with split
-partitions) behind the C ABI of include/ikl_paged.h, with the reference's
-operator surface (ops), paged cache (cache), scheduler and runtime hooks,
-and the decode runners that call them (decode: synthetic decoder; llama:
-Llama over the paged cache).
+Hand-written HIP kernels (KV append, fused RoPE + append, paged decode
+attention with split partitions, paged prefill attention) behind the C ABI
+of include/ikl_paged.h, with the reference's operator surface (ops), paged
+cache (cache), scheduler and runtime hooks, and the decode runners that
+call them (decode: synthetic decoder; llama: Llama over the paged cache).
 """
 
 from .cache import BlockAllocator, CacheLayout, PagedKVCache
@@ -21,6 +21,9 @@ from .ops import (
     paged_decode_grouped_autotune_config,
     paged_decode_grouped_dot_autotune_config,
     paged_decode_grouped_path,
+    paged_prefill_attention_hip,
+    paged_prefill_path,
+    PreparedPagedPrefill,
     rope_append_kv_hip,
     triton_append_available,
     triton_available,
@@ -46,6 +49,9 @@ __all__ = [
     "paged_decode_attention_triton",
     "paged_decode_attention_triton_grouped",
     "paged_decode_grouped_path",
+    "paged_prefill_attention_hip",
+    "paged_prefill_path",
+    "PreparedPagedPrefill",
     "rope_append_kv_hip",
     "paged_decode_autotune_config",
     "paged_decode_grouped_autotune_config",

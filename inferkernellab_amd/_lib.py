@@ -33,6 +33,8 @@ EXPORTED_SYMBOLS = (
     "ikl_paged_attention_path",
     "ikl_paged_attention_launch_config",
     "ikl_rope_append_kv",
+    "ikl_paged_prefill_attention",
+    "ikl_paged_prefill_path",
 )
 
 _c_i64 = ctypes.c_int64
@@ -151,6 +153,47 @@ class RopeAppendArgs(ctypes.Structure):
     ]
 
 
+class PagedPrefillArgs(ctypes.Structure):
+    """Mirror of ikl_paged_prefill_args."""
+
+    _fields_ = [
+        ("query", _c_ptr),
+        ("q_stride_b", _c_i64),
+        ("q_stride_h", _c_i64),
+        ("q_stride_t", _c_i64),
+        ("k_cache", _c_ptr),
+        ("v_cache", _c_ptr),
+        ("k_stride_block", _c_i64),
+        ("k_stride_token", _c_i64),
+        ("k_stride_head", _c_i64),
+        ("v_stride_block", _c_i64),
+        ("v_stride_token", _c_i64),
+        ("v_stride_head", _c_i64),
+        ("block_tables", _c_ptr),
+        ("table_type", _c_i32),
+        ("table_stride_b", _c_i64),
+        ("table_width", _c_i64),
+        ("query_starts", _c_ptr),
+        ("context_lens", _c_ptr),
+        ("lens_type", _c_i32),
+        ("out", _c_ptr),
+        ("out_stride_b", _c_i64),
+        ("out_stride_h", _c_i64),
+        ("out_stride_t", _c_i64),
+        ("batch", _c_i64),
+        ("query_width", _c_i64),
+        ("num_blocks", _c_i64),
+        ("num_heads", _c_i32),
+        ("num_kv_heads", _c_i32),
+        ("head_dim", _c_i32),
+        ("block_size", _c_i32),
+        ("dtype", _c_i32),
+        ("scale", ctypes.c_float),
+        ("path", _c_i32),
+        ("events", _c_ptr * 2),
+    ]
+
+
 class LaunchConfig(ctypes.Structure):
     """Mirror of ikl_launch_config."""
 
@@ -187,6 +230,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ikl_paged_attention_path.argtypes = [_c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32]
     lib.ikl_rope_append_kv.restype = ctypes.c_int
     lib.ikl_rope_append_kv.argtypes = [ctypes.POINTER(RopeAppendArgs), _c_ptr]
+    lib.ikl_paged_prefill_attention.restype = ctypes.c_int
+    lib.ikl_paged_prefill_attention.argtypes = [ctypes.POINTER(PagedPrefillArgs), _c_ptr]
+    lib.ikl_paged_prefill_path.restype = _c_i32
+    lib.ikl_paged_prefill_path.argtypes = [_c_i32, _c_i32, _c_i32]
     lib.ikl_paged_attention_launch_config.restype = ctypes.c_int
     lib.ikl_paged_attention_launch_config.argtypes = [ctypes.POINTER(PagedAttentionArgs),
                                                       ctypes.POINTER(LaunchConfig)]

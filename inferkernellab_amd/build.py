@@ -21,7 +21,14 @@ LIB_NAME = "libikl_paged.so"
 LIB_PATH = PACKAGE_DIR / LIB_NAME
 ARCH = "gfx950"
 
-SOURCES = ("abi.hip", "append_kv.hip", "paged_decode.hip", "paged_decode_mfma.hip", "rope_append.hip")
+SOURCES = (
+    "abi.hip",
+    "append_kv.hip",
+    "paged_decode.hip",
+    "paged_decode_mfma.hip",
+    "paged_prefill.hip",
+    "rope_append.hip",
+)
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -26,27 +26,13 @@
 //    of the batch's global tile sequence (see AttnParams::sk_waves), so every
 //    wave starts once, streams ~T/W tiles and all finish together.
 //
-// MFMA operand layouts (gfx950; 16x16x32 checked by a lane-layout probe):
-//   16x16x32: lane l supplies A[l%16][8(l/16)+j], B[8(l/16)+j][l%16], j < 8;
-//   16x16x16: lane l supplies A[l%16][4(l/16)+j], B[4(l/16)+j][l%16], j < 4;
-//   both:     lane l receives D[4(l/16)+i][l%16], i < 4.
-// ds_read_b64_tr_b16: in each 16-lane group, lane i receives element i%4 of
-//   the 8-byte chunks supplied by lanes 4k + i/4, k < 4.
+// MFMA operand layouts and the transposing LDS read: see mfma_ops.h.
 #include "ikl_common.h"
+#include "mfma_ops.h"
 #include "paged_attn.h"
 
 namespace ikl {
 namespace {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int TILE = 16;  // tokens per tile
 
@@ -67,49 +53,11 @@ constexpr int TILE = 16;  // tokens per tile
 #define IKL_MFMA_WAVES_ATTR __attribute__((amdgpu_waves_per_eu(IKL_MFMA_MIN_WAVES, 8)))
 #endif
 
+// bf16 P with its rounding residual in a second MFMA (fp16 P is not split).
 template <typename Tag>
-struct mfma_ops;
-
-template <>
-struct mfma_ops<bf16_tag> {
-  // S^T tile: K[16 x 32] . Q^T[32 x 16]
-  __device__ static inline f32x4_t mma_k32(v4u32 a, v4u32 b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-  }
-  // O^T tile: V^T[16 x 16] . P[16 x 16]
-  __device__ static inline f32x4_t mma_k16(u32x2_t a, u32x2_t b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a),
-                                                     __builtin_bit_cast(s16x4_t, b), c, 0, 0, 0);
-  }
-  // Round-to-nearest-even pack of two probabilities (v_cvt_pk_bf16_f32).
-  __device__ static inline uint32_t pack(float x, float y) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{x, y}, bf16x2_t));
-  }
-  __device__ static inline float lo(uint32_t w) { return __uint_as_float(w << 16); }
-  __device__ static inline float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-  static constexpr bool SPLIT_P = IKL_MFMA_SPLIT_P != 0;
-};
-
-template <>
-struct mfma_ops<f16_tag> {
-  __device__ static inline f32x4_t mma_k32(v4u32 a, v4u32 b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
-                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
-  }
-  __device__ static inline f32x4_t mma_k16(u32x2_t a, u32x2_t b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a),
-                                                 __builtin_bit_cast(f16x4_t, b), c, 0, 0, 0);
-  }
-  __device__ static inline uint32_t pack(float x, float y) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{x, y}, f16x2_t));
-  }
-  __device__ static inline float lo(uint32_t w) { return (float)__builtin_bit_cast(f16x2_t, w)[0]; }
-  __device__ static inline float hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2_t, w)[1]; }
-  static constexpr bool SPLIT_P = false;  // fp16 P (<= 2^8) already keeps 11 bits
-};
-
-__device__ inline v4u32 zero4() { return v4u32{0u, 0u, 0u, 0u}; }
+constexpr bool split_p() {
+  return IKL_MFMA_SPLIT_P != 0 && mfma_ops<Tag>::NARROW_P;
+}
 
 // Per-wave state of the tile loop: lane constants, the Q^T operands and the
 // running softmax states (acc, m, lsum) of one (request, unit) run. A unit
@@ -271,7 +219,7 @@ struct WaveTiles {
         // A bf16 P keeps 8 significant bits; with SPLIT_P its rounding
         // residual P - bf16(P) goes through a second MFMA, so P enters with
         // ~16 bits (as the fp32 P of the reference's kernels).
-        if constexpr (ops::SPLIT_P)
+        if constexpr (split_p<Tag>())
           pl[g] = u32x2_t{ops::pack(pr[0] - ops::lo(pb[g].x), pr[1] - ops::hi(pb[g].x)),
                           ops::pack(pr[2] - ops::lo(pb[g].y), pr[3] - ops::hi(pb[g].y))};
       }
@@ -279,13 +227,12 @@ struct WaveTiles {
       s16x4_t va[MTILES];
 #pragma unroll
       for (int mt = 0; mt < MTILES; ++mt) {
-        typedef __attribute__((address_space(3))) s16x4_t *lds_s4_ptr;
-        va[mt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_ptr)(vtile + tr_lds[mt]));
+        va[mt] = __builtin_bit_cast(s16x4_t, lds_read_tr(vtile + tr_lds[mt]));
 #pragma unroll
         for (int g = 0; g < NG; ++g)
           acc[g][mt] = ops::mma_k16(__builtin_bit_cast(u32x2_t, va[mt]), pb[g], acc[g][mt]);
       }
-      if constexpr (ops::SPLIT_P) {
+      if constexpr (split_p<Tag>()) {
 #pragma unroll
         for (int mt = 0; mt < MTILES; ++mt)
 #pragma unroll

@@ -1,0 +1,604 @@
+// Paged prefill attention: causal attention of a ragged batch of prompt
+// chunks over the block-table addressed cache. Same result as the gather +
+// masked SDPA of paged_prefill_attention_sdpa (attention.py:230-321):
+//
+//   row t of request b sits at position start_b + t; rows t < len_b - start_b
+//   attend the keys at positions <= start_b + t (all < len_b); the remaining
+//   (padding) rows of the query width receive the value at position 0, which
+//   is what the reference's mask leaves them (attention.py:305).
+//
+// Two kernel families:
+//
+//  * MFMA (fp16 / bf16, head_dim 32k <= 128, block_size % 16 == 0):
+//    paged_prefill_mfma_kernel. A workgroup of 4 waves takes 64 * NG query
+//    rows of one (request, kv head) — a row is one (token, query head) pair,
+//    token-major, so the heads sharing a KV head sit in consecutive rows —
+//    and streams the request's keys in 32-token tiles that the workgroup
+//    stages once in LDS for all its waves (double-buffered, one barrier per
+//    tile). Each wave owns 16 * NG rows and runs, per tile and 16-row group:
+//
+//      S^T[32 keys x 16 rows] = K . Q^T     2 * D/32 v_mfma_f32_16x16x32
+//      online softmax (lane = one row x 8 keys, causal mask on the diagonal)
+//      O^T[D x 16 rows]     += V^T . P      D/16 v_mfma_f32_16x16x32
+//
+//    Both products use the full-rate gfx950 16x16x32 shape: the K rows of the
+//    two S^T halves are permuted (MFMA row 4g + i of half h holds key
+//    8g + 4h + i) so that lane l ends with the scores of keys 8(l/16)..+7,
+//    exactly the P operand of a 32-deep PV MFMA; its V^T operand is two
+//    ds_read_b64_tr_b16 of the staged tile.
+//
+//  * VALU (every other dtype / head_dim <= 256 / block size):
+//    paged_prefill_scalar_kernel, one wave per (request, head, row), keys in
+//    sequence, fp32 online softmax.
+//
+// Blocks whose table entry lies outside [0, num_blocks) are masked as in the
+// decode kernels; no load ever leaves the cache.
+#include "ikl_common.h"
+#include "mfma_ops.h"
+#include "paged_attn.h"
+
+namespace ikl {
+
+struct PrefillParams {
+  const char *q;
+  int64_t q_sb, q_sh, q_st;  // elements
+  const char *kc;
+  const char *vc;
+  int64_t k_sb, k_st, k_sh;
+  int64_t v_sb, v_st, v_sh;
+  const void *tables;
+  int64_t t_sb;
+  int64_t table_width;
+  const void *starts;
+  const void *lens;
+  char *out;
+  int64_t o_sb, o_sh, o_st;
+  int64_t batch;
+  int64_t width;       // query rows per request (T)
+  int64_t num_blocks;
+  int64_t cap_tokens;  // table_width * block_size
+  int64_t row_blocks;  // workgroups per (request, kv head) of the MFMA kernel
+  int64_t bh_pad;      // batch * num_kv_heads rounded up to a multiple of 8
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t heads_per_kv;
+  int32_t head_dim;
+  int32_t block_size;
+  int32_t bs_shift;  // log2(block_size) or -1
+  int32_t table_i64;
+  int32_t idx_i64;   // starts / lens element type
+  float scale_log2;  // scale * log2(e)
+};
+
+namespace {
+
+__device__ inline int64_t pf_index(const void *base, int64_t i, int i64) {
+  return i64 ? load_index<int64_t>(base, i) : load_index<int32_t>(base, i);
+}
+
+// Block-table entry (b, lb), or -1 when it is outside the table or names a
+// block outside the cache.
+__device__ inline int pf_block(const PrefillParams &p, int64_t b, int64_t lb) {
+  if (lb < 0 || lb >= p.table_width) return -1;
+  const int64_t e = pf_index(p.tables, b * p.t_sb + lb, p.table_i64);
+  return e >= 0 && e < p.num_blocks ? (int)e : -1;
+}
+
+// Prefill range of request b: start (clamped to [0, end]), end (clamped to
+// [0, cap_tokens]) and the number of attending rows (<= width).
+__device__ inline void pf_range(const PrefillParams &p, int64_t b, int64_t *start, int64_t *end, int64_t *rows) {
+  int64_t e = pf_index(p.lens, b, p.idx_i64);
+  e = e < 0 ? 0 : (e < p.cap_tokens ? e : p.cap_tokens);
+  int64_t s = pf_index(p.starts, b, p.idx_i64);
+  s = s < 0 ? 0 : (s < e ? s : e);
+  *start = s;
+  *end = e;
+  *rows = e - s < p.width ? e - s : p.width;
+}
+
+__device__ inline int64_t pf_logical(const PrefillParams &p, int64_t pos) {
+  return p.bs_shift >= 0 ? (pos >> p.bs_shift) : pos / p.block_size;
+}
+
+constexpr int PT = 32;     // keys per tile
+constexpr int PWAVES = 4;  // waves per workgroup
+
+#ifndef IKL_PREFILL_NG
+#define IKL_PREFILL_NG 4
+#endif
+#ifndef IKL_PREFILL_SPLIT_P
+#define IKL_PREFILL_SPLIT_P 0
+#endif
+
+template <typename Tag, int D, int NG>
+__global__ __launch_bounds__(64 * PWAVES) void paged_prefill_mfma_kernel(const PrefillParams p) {
+  static_assert(D % 32 == 0 && D <= 128, "MFMA prefill needs head_dim = 32k <= 128");
+  using ops = mfma_ops<Tag>;
+  constexpr bool SPLIT = IKL_PREFILL_SPLIT_P != 0 && ops::NARROW_P;
+  constexpr int EB = 2;
+  constexpr int ROWB = D * EB;               // bytes per K/V row
+  constexpr int PIECES = ROWB / 16;          // 16-byte pieces per row
+  constexpr int KSTEPS = D / 32;             // QK^T k-steps
+  constexpr int MTILES = D / 16;             // PV output tiles of 16 dims
+  constexpr int RW = 16 * NG;                // query rows per wave
+  constexpr int RWG = RW * PWAVES;           // query rows per workgroup
+  constexpr int TILE_BYTES = PT * ROWB;      // one staged K or V tile
+  constexpr int NTHREADS = 64 * PWAVES;
+  constexpr int LP = (PT * PIECES + NTHREADS - 1) / NTHREADS;  // pieces per thread per tile
+  __shared__ __attribute__((aligned(16))) char lds[2][2][TILE_BYTES];  // [stage][K, V]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, hl = lane & 15, grp = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // Workgroup -> (row block, request, kv head). All row blocks of one
+  // (request, kv head) share blockIdx.x mod 8, hence one XCD and its L2; the
+  // row blocks nearest the end of the prompts (most keys) start first.
+  const int64_t idx = blockIdx.x;
+  const int64_t bh = idx % p.bh_pad;
+  if (bh >= p.batch * p.num_kv_heads) return;
+  const int64_t rb = p.row_blocks - 1 - idx / p.bh_pad;
+  const int64_t b = bh / p.num_kv_heads;
+  const int kvh = (int)(bh % p.num_kv_heads);
+  const int G = p.heads_per_kv;
+
+  int64_t start, end, nrows;
+  pf_range(p, b, &start, &end, &nrows);
+  const int64_t rows_valid = nrows * G, rows_all = p.width * G;
+  const int64_t row0 = rb * RWG;
+  const int64_t wr0 = row0 + (int64_t)wave * RW;
+
+  // keys the workgroup needs, and the wave's own causal window
+  const int64_t wg_last = (row0 + RWG < rows_valid ? row0 + RWG : rows_valid) - 1;
+  const int64_t kv_hi = wg_last >= row0 ? start + wg_last / G + 1 : 0;
+  const int n_tiles = (int)((kv_hi + PT - 1) / PT);
+  const int64_t w_last = (wr0 + RW < rows_valid ? wr0 + RW : rows_valid) - 1;
+  const int64_t w_hi = w_last >= wr0 ? start + w_last / G + 1 : 0;  // keys [0, w_hi) reach some row
+  const int64_t w_lo = start + wr0 / G;                             // every row sees keys <= w_lo
+
+  // Q^T operands and the position of each lane's row (-1: not attending)
+  v4u32 qb[NG][KSTEPS];
+  int64_t qpos[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    const int64_t r = wr0 + 16 * g + hl;
+    const bool ok = r < rows_valid;
+    const int64_t t = ok ? r / G : 0;
+    const int h = ok ? (int)(r % G) : 0;
+    qpos[g] = ok ? start + t : -1;
+    const char *qrow = p.q + (b * p.q_sb + ((int64_t)kvh * G + h) * p.q_sh + t * p.q_st + 8 * grp) * EB;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) qb[g][s] = ok ? load16v_global(qrow + 64 * s) : zero4();
+  }
+
+  f32x4_t acc[NG][MTILES];
+  float m[NG], lsum[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+#pragma unroll
+    for (int mt = 0; mt < MTILES; ++mt) acc[g][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    m[g] = NEG_SENTINEL;
+    lsum[g] = 0.f;
+  }
+
+  // LDS offsets (pieces rotated by row): the K rows of the two S^T halves,
+  // the V^T chunks, and this thread's share of the cooperative tile copy.
+  const int kappa = 8 * (hl >> 2) + (hl & 3);  // key of MFMA row hl in half 0 (+4 in half 1)
+  int k_off[2][KSTEPS], tr_off[2][MTILES];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int row = kappa + 4 * h;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) k_off[h][s] = row * ROWB + ((4 * s + grp + row) % PIECES) * 16;
+    const int vrow = 8 * grp + 4 * h + (hl >> 2);
+#pragma unroll
+    for (int mt = 0; mt < MTILES; ++mt) {
+      const int c = 2 * mt + ((hl & 3) >> 1);
+      tr_off[h][mt] = vrow * ROWB + ((c + vrow) % PIECES) * 16 + (hl & 1) * 8;
+    }
+  }
+  int cp_row[LP], cp_lds[LP];
+#pragma unroll
+  for (int u = 0; u < LP; ++u) {
+    const int pi = u * NTHREADS + tid;
+    const int row = pi / PIECES, c = pi % PIECES;
+    cp_row[u] = pi < PT * PIECES ? row : -1;
+    cp_lds[u] = row * ROWB + ((c + row) % PIECES) * 16;
+  }
+
+  const char *kbase = p.kc + (int64_t)kvh * p.k_sh * EB;
+  const char *vbase = p.vc + (int64_t)kvh * p.v_sh * EB;
+  v4u32 rk[LP], rv[LP];
+  uint32_t next_mask = 0;
+
+  // Global -> registers for tile j; returns the tile's valid-key bitmask
+  // (position < end and a block inside the cache).
+  auto fetch = [&](int j) -> uint32_t {
+    const int64_t base = (int64_t)j * PT;
+    const int64_t lb0 = pf_logical(p, base), lb1 = pf_logical(p, base + 16);
+    const int ph0 = pf_block(p, b, lb0), ph1 = pf_block(p, b, lb1);
+    const int64_t left = end - base;
+    uint32_t mask = (ph0 >= 0 ? 0xffffu : 0u) | (ph1 >= 0 ? 0xffff0000u : 0u);
+    if (left < PT) mask &= left > 0 ? (1u << left) - 1u : 0u;
+#pragma unroll
+    for (int u = 0; u < LP; ++u) {
+      const int row = cp_row[u];
+      const bool half = row >= 16;
+      const int ph = half ? ph1 : ph0;
+      const int64_t lb = half ? lb1 : lb0;
+      const bool ok = row >= 0 && ((mask >> (row & 31)) & 1u);
+      const int64_t off = base + row - lb * p.block_size;
+      const int c16 = (tid + u * NTHREADS) % PIECES * 16;
+      rk[u] = ok ? load16v_global(kbase + ((int64_t)ph * p.k_sb + off * p.k_st) * EB + c16) : zero4();
+      rv[u] = ok ? load16v_global(vbase + ((int64_t)ph * p.v_sb + off * p.v_st) * EB + c16) : zero4();
+    }
+    return mask;
+  };
+
+  auto compute = [&](const char *kt, const char *vt, int64_t base, uint32_t mask) {
+    if (base >= w_hi) return;  // no row of this wave reaches the tile
+    const bool masked = mask != 0xffffffffu || base + PT - 1 > w_lo;
+    v4u32 ka[2][KSTEPS];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) ka[h][s] = *reinterpret_cast<const v4u32 *>(kt + k_off[h][s]);
+    v4u32 pb[NG], pl[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      f32x4_t s0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        s0 = ops::mma_k32(ka[0][s], qb[g][s], s0);
+        s1 = ops::mma_k32(ka[1][s], qb[g][s], s1);
+      }
+      // lane: row hl of group g, keys 8 grp + j (j < 4 from s0, 4.. from s1)
+      float sc[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[i] = s0[i] * p.scale_log2;
+        sc[4 + i] = s1[i] * p.scale_log2;
+      }
+      if (masked) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int key = 8 * grp + j;
+          const bool ok = ((mask >> key) & 1u) && base + key <= qpos[g];
+          sc[j] = ok ? sc[j] : -INFINITY;
+        }
+      }
+      float tmax = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
+                         fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+      tmax = max_xor32(max_xor16(tmax));
+      const bool need = tmax > m[g] + RESCALE_LOG2;
+      if (__builtin_amdgcn_ballot_w64(need) != 0ull) {
+        const float alpha = need ? fast_exp2(m[g] - tmax) : 1.f;
+        m[g] = need ? tmax : m[g];
+        lsum[g] *= alpha;
+#pragma unroll
+        for (int mt = 0; mt < MTILES; ++mt) acc[g][mt] *= alpha;
+      }
+      float pr[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        pr[j] = fast_exp2(sc[j] - m[g]);
+        lsum[g] += pr[j];
+      }
+      pb[g] = v4u32{ops::pack(pr[0], pr[1]), ops::pack(pr[2], pr[3]), ops::pack(pr[4], pr[5]),
+                    ops::pack(pr[6], pr[7])};
+      if constexpr (SPLIT) {
+        pl[g] = v4u32{ops::pack(pr[0] - ops::lo(pb[g].x), pr[1] - ops::hi(pb[g].x)),
+                      ops::pack(pr[2] - ops::lo(pb[g].y), pr[3] - ops::hi(pb[g].y)),
+                      ops::pack(pr[4] - ops::lo(pb[g].z), pr[5] - ops::hi(pb[g].z)),
+                      ops::pack(pr[6] - ops::lo(pb[g].w), pr[7] - ops::hi(pb[g].w))};
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MTILES; ++mt) {
+      const u32x2_t v0 = lds_read_tr(vt + tr_off[0][mt]), v1 = lds_read_tr(vt + tr_off[1][mt]);
+      const v4u32 va = v4u32{v0.x, v0.y, v1.x, v1.y};  // V^T[16mt + hl][keys 8 grp .. +7]
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        acc[g][mt] = ops::mma_k32(va, pb[g], acc[g][mt]);
+        if constexpr (SPLIT) acc[g][mt] = ops::mma_k32(va, pl[g], acc[g][mt]);
+      }
+    }
+  };
+
+  if (n_tiles > 0) next_mask = fetch(0);
+  for (int j = 0; j < n_tiles; ++j) {
+    const int st = j & 1;
+    char *kt = lds[st][0];
+    char *vt = lds[st][1];
+#pragma unroll
+    for (int u = 0; u < LP; ++u) {
+      if (cp_row[u] >= 0) {
+        *reinterpret_cast<v4u32 *>(kt + cp_lds[u]) = rk[u];
+        *reinterpret_cast<v4u32 *>(vt + cp_lds[u]) = rv[u];
+      }
+    }
+    const uint32_t mask = next_mask;
+    __syncthreads();
+    if (j + 1 < n_tiles) next_mask = fetch(j + 1);
+    compute(kt, vt, (int64_t)j * PT, mask);
+  }
+
+  // Normalise and store. Lane (hl, grp) holds O^T[16 mt + 4 grp + i][row hl].
+#pragma unroll
+  for (int g = 0; g < NG; ++g) lsum[g] = sum_xor32(sum_xor16(lsum[g]));
+  const int ph_first = pf_block(p, b, 0);
+  const char *v0row = ph_first >= 0 && end > 0 ? vbase + (int64_t)ph_first * p.v_sb * EB : nullptr;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    const int64_t r = wr0 + 16 * g + hl;
+    if (r >= rows_all) continue;
+    const int64_t t = r / G;
+    const int h = (int)(r % G);
+    char *dst = p.out + (b * p.o_sb + ((int64_t)kvh * G + h) * p.o_sh + t * p.o_st + 4 * grp) * EB;
+    if (r < rows_valid) {
+      const float inv = 1.f / lsum[g];  // no attended key: 0/0 -> NaN
+#pragma unroll
+      for (int mt = 0; mt < MTILES; ++mt) {
+        const f32x4_t o = acc[g][mt] * inv;
+        const u32x2_t w = u32x2_t{ops::pack(o[0], o[1]), ops::pack(o[2], o[3])};
+        *reinterpret_cast<u32x2_t *>(dst + 32 * mt) = w;
+      }
+    } else {
+      // padding row: the value at position 0 (zero when its block is masked)
+#pragma unroll
+      for (int mt = 0; mt < MTILES; ++mt) {
+        u32x2_t w = u32x2_t{0u, 0u};
+        if (v0row) w = *reinterpret_cast<const u32x2_t *>(v0row + (16 * mt + 4 * grp) * EB);
+        *reinterpret_cast<u32x2_t *>(dst + 32 * mt) = w;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ VALU
+// One wave per (request, head, row). The lanes split the row's head_dim in
+// 4-byte granules (one fp32 or two 16-bit elements; up to 4 per lane), walk
+// the keys in order and keep an fp32 online softmax in the log2 domain.
+template <typename Tag>
+struct granule;
+template <>
+struct granule<f32_tag> {
+  static constexpr int EB = 4, PER = 1;
+  __device__ static inline void unpack(uint32_t w, float *x) { x[0] = __uint_as_float(w); }
+  __device__ static inline uint32_t pack(const float *x) { return __float_as_uint(x[0]); }
+};
+template <>
+struct granule<bf16_tag> {
+  static constexpr int EB = 2, PER = 2;
+  __device__ static inline void unpack(uint32_t w, float *x) {
+    x[0] = elem<bf16_tag>::lo(w);
+    x[1] = elem<bf16_tag>::hi(w);
+  }
+  __device__ static inline uint32_t pack(const float *x) { return elem<bf16_tag>::pack2(x[0], x[1]); }
+};
+template <>
+struct granule<f16_tag> {
+  static constexpr int EB = 2, PER = 2;
+  __device__ static inline void unpack(uint32_t w, float *x) {
+    x[0] = elem<f16_tag>::lo(w);
+    x[1] = elem<f16_tag>::hi(w);
+  }
+  __device__ static inline uint32_t pack(const float *x) { return elem<f16_tag>::pack2(x[0], x[1]); }
+};
+
+__device__ inline float wave_sum(float v) { return sum_xor32(sum_xor16(group_sum<16>(v))); }
+
+template <typename Tag>
+__global__ __launch_bounds__(64) void paged_prefill_scalar_kernel(const PrefillParams p) {
+  using GR = granule<Tag>;
+  constexpr int EB = GR::EB, PER = GR::PER, MAXG = 4;
+  const int lane = threadIdx.x;
+  const int64_t idx = blockIdx.x;
+  const int64_t t = idx % p.width;
+  const int h = (int)((idx / p.width) % p.num_heads);
+  const int64_t b = idx / (p.width * p.num_heads);
+  const int kvh = h / p.heads_per_kv;
+  const int ngr = p.head_dim * EB / 4;  // granules per row (<= 256)
+
+  int64_t start, end, nrows;
+  pf_range(p, b, &start, &end, &nrows);
+  uint32_t *dst = reinterpret_cast<uint32_t *>(p.out + (b * p.o_sb + (int64_t)h * p.o_sh + t * p.o_st) * EB);
+  const char *kbase = p.kc + (int64_t)kvh * p.k_sh * EB;
+  const char *vbase = p.vc + (int64_t)kvh * p.v_sh * EB;
+
+  if (t >= nrows) {  // padding row: the value at position 0
+    const int ph = end > 0 ? pf_block(p, b, 0) : -1;
+    const uint32_t *src = ph >= 0 ? reinterpret_cast<const uint32_t *>(vbase + (int64_t)ph * p.v_sb * EB) : nullptr;
+    for (int gi = lane; gi < ngr; gi += 64) dst[gi] = src ? src[gi] : 0u;
+    return;
+  }
+
+  float q[MAXG][PER], acc[MAXG][PER];
+  const uint32_t *qrow = reinterpret_cast<const uint32_t *>(p.q + (b * p.q_sb + (int64_t)h * p.q_sh + t * p.q_st) * EB);
+#pragma unroll
+  for (int k = 0; k < MAXG; ++k) {
+    const int gi = lane + 64 * k;
+    GR::unpack(gi < ngr ? qrow[gi] : 0u, q[k]);
+#pragma unroll
+    for (int e = 0; e < PER; ++e) acc[k][e] = 0.f;
+  }
+  float m = NEG_SENTINEL, l = 0.f;
+  const int64_t kend = start + t + 1;
+  int64_t cur_lb = -1;
+  int ph = -1;
+  for (int64_t kp = 0; kp < kend; ++kp) {
+    const int64_t lb = pf_logical(p, kp);
+    if (lb != cur_lb) {
+      cur_lb = lb;
+      ph = pf_block(p, b, lb);
+    }
+    if (ph < 0) continue;
+    const int64_t off = kp - lb * p.block_size;
+    const uint32_t *krow = reinterpret_cast<const uint32_t *>(kbase + ((int64_t)ph * p.k_sb + off * p.k_st) * EB);
+    const uint32_t *vrow = reinterpret_cast<const uint32_t *>(vbase + ((int64_t)ph * p.v_sb + off * p.v_st) * EB);
+    float s = 0.f;
+    float vv[MAXG][PER];
+#pragma unroll
+    for (int k = 0; k < MAXG; ++k) {
+      const int gi = lane + 64 * k;
+      float kx[PER];
+      GR::unpack(gi < ngr ? krow[gi] : 0u, kx);
+      GR::unpack(gi < ngr ? vrow[gi] : 0u, vv[k]);
+#pragma unroll
+      for (int e = 0; e < PER; ++e) s = fmaf(q[k][e], kx[e], s);
+    }
+    s = wave_sum(s) * p.scale_log2;
+    const float mn = fmaxf(m, s);
+    const float alpha = fast_exp2(m - mn), pr = fast_exp2(s - mn);
+    l = l * alpha + pr;
+#pragma unroll
+    for (int k = 0; k < MAXG; ++k)
+#pragma unroll
+      for (int e = 0; e < PER; ++e) acc[k][e] = acc[k][e] * alpha + pr * vv[k][e];
+    m = mn;
+  }
+  const float inv = 1.f / l;  // no attended key: 0/0 -> NaN
+#pragma unroll
+  for (int k = 0; k < MAXG; ++k) {
+    const int gi = lane + 64 * k;
+    if (gi >= ngr) continue;
+    float o[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) o[e] = acc[k][e] * inv;
+    dst[gi] = GR::pack(o);
+  }
+}
+
+template <typename Tag, int NG>
+hipError_t launch_mfma_dim(int d, const PrefillParams &p, dim3 grid, hipStream_t s) {
+  switch (d) {
+    case 32: paged_prefill_mfma_kernel<Tag, 32, NG><<<grid, 64 * PWAVES, 0, s>>>(p); break;
+    case 64: paged_prefill_mfma_kernel<Tag, 64, NG><<<grid, 64 * PWAVES, 0, s>>>(p); break;
+    case 96: paged_prefill_mfma_kernel<Tag, 96, NG><<<grid, 64 * PWAVES, 0, s>>>(p); break;
+    default: paged_prefill_mfma_kernel<Tag, 128, NG><<<grid, 64 * PWAVES, 0, s>>>(p); break;
+  }
+  return hipGetLastError();
+}
+
+bool prefill_mfma_supported(int dtype, int head_dim, int block_size) {
+  return (dtype == IKL_F16 || dtype == IKL_BF16) &&
+         (head_dim == 32 || head_dim == 64 || head_dim == 96 || head_dim == 128) && block_size > 0 &&
+         block_size % 16 == 0;
+}
+
+bool aligned(const void *ptr, int64_t bytes) { return ((uintptr_t)ptr) % bytes == 0; }
+
+}  // namespace
+}  // namespace ikl
+
+using namespace ikl;
+
+extern "C" int32_t ikl_paged_prefill_path(int32_t dtype, int32_t head_dim, int32_t block_size) {
+  return prefill_mfma_supported(dtype, head_dim, block_size) ? IKL_PATH_MFMA_GROUPED : IKL_PATH_SCALAR_GROUPED;
+}
+
+extern "C" int ikl_paged_prefill_attention(const ikl_paged_prefill_args *a, void *stream) {
+  if (!a) return fail(IKL_EINVAL, "ikl_paged_prefill_attention: args is NULL");
+  if (a->batch <= 0 || a->query_width <= 0 || a->num_heads <= 0 || a->num_kv_heads <= 0 || a->head_dim <= 0 ||
+      a->block_size <= 0 || a->num_blocks <= 0 || a->table_width <= 0)
+    return fail(IKL_EINVAL, "ikl_paged_prefill_attention: sizes must be positive");
+  if (a->num_heads % a->num_kv_heads != 0)
+    return fail(IKL_EINVAL, "ikl_paged_prefill_attention: num_heads must be divisible by num_kv_heads");
+  if (a->dtype != IKL_F16 && a->dtype != IKL_BF16 && a->dtype != IKL_F32)
+    return fail(IKL_EINVAL, "ikl_paged_prefill_attention: unknown dtype");
+  if ((a->table_type != IKL_I32 && a->table_type != IKL_I64) || (a->lens_type != IKL_I32 && a->lens_type != IKL_I64))
+    return fail(IKL_EINVAL, "ikl_paged_prefill_attention: unknown index type");
+  if (!a->query || !a->k_cache || !a->v_cache || !a->block_tables || !a->query_starts || !a->context_lens || !a->out)
+    return fail(IKL_EINVAL, "ikl_paged_prefill_attention: NULL tensor pointer");
+  const int eb = a->dtype == IKL_F32 ? 4 : 2;
+  if (a->head_dim * eb % 4 != 0 || a->head_dim * eb > 1024)
+    return fail(IKL_EUNSUPPORTED, "ikl_paged_prefill_attention: head_dim must give rows of 4k <= 1024 bytes");
+  if (a->table_width > (int64_t(1) << 40) / a->block_size)
+    return fail(IKL_EINVAL, "ikl_paged_prefill_attention: table_width * block_size is too large");
+
+  const int auto_path = ikl_paged_prefill_path(a->dtype, a->head_dim, a->block_size);
+  const int path = a->path < 0 ? auto_path : a->path;
+  if (path != IKL_PATH_MFMA_GROUPED && path != IKL_PATH_SCALAR_GROUPED)
+    return fail(IKL_EINVAL, "ikl_paged_prefill_attention: path must be -1, IKL_PATH_SCALAR_GROUPED or IKL_PATH_MFMA_GROUPED");
+  if (path == IKL_PATH_MFMA_GROUPED && auto_path != IKL_PATH_MFMA_GROUPED)
+    return fail(IKL_EUNSUPPORTED, "ikl_paged_prefill_attention: no MFMA kernel for this dtype / head_dim / block_size");
+
+  // every row the kernels touch must be aligned to its access width
+  const int64_t align = path == IKL_PATH_MFMA_GROUPED ? 16 : 4;
+  const int64_t out_align = path == IKL_PATH_MFMA_GROUPED ? 8 : 4;
+  const int64_t in_strides[] = {a->q_stride_b, a->q_stride_h, a->q_stride_t, a->k_stride_block, a->k_stride_token,
+                                a->k_stride_head, a->v_stride_block, a->v_stride_token, a->v_stride_head};
+  for (int64_t st : in_strides)
+    if ((st * eb) % align != 0) return fail(IKL_EINVAL, "ikl_paged_prefill_attention: misaligned input stride");
+  const int64_t out_strides[] = {a->out_stride_b, a->out_stride_h, a->out_stride_t};
+  for (int64_t st : out_strides)
+    if ((st * eb) % out_align != 0) return fail(IKL_EINVAL, "ikl_paged_prefill_attention: misaligned output stride");
+  if (!aligned(a->query, align) || !aligned(a->k_cache, align) || !aligned(a->v_cache, align) ||
+      !aligned(a->out, out_align))
+    return fail(IKL_EINVAL, "ikl_paged_prefill_attention: misaligned tensor pointer");
+
+  PrefillParams p{};
+  p.q = static_cast<const char *>(a->query);
+  p.q_sb = a->q_stride_b;
+  p.q_sh = a->q_stride_h;
+  p.q_st = a->q_stride_t;
+  p.kc = static_cast<const char *>(a->k_cache);
+  p.vc = static_cast<const char *>(a->v_cache);
+  p.k_sb = a->k_stride_block;
+  p.k_st = a->k_stride_token;
+  p.k_sh = a->k_stride_head;
+  p.v_sb = a->v_stride_block;
+  p.v_st = a->v_stride_token;
+  p.v_sh = a->v_stride_head;
+  p.tables = a->block_tables;
+  p.t_sb = a->table_stride_b;
+  p.table_width = a->table_width;
+  p.starts = a->query_starts;
+  p.lens = a->context_lens;
+  p.out = static_cast<char *>(a->out);
+  p.o_sb = a->out_stride_b;
+  p.o_sh = a->out_stride_h;
+  p.o_st = a->out_stride_t;
+  p.batch = a->batch;
+  p.width = a->query_width;
+  p.num_blocks = a->num_blocks;
+  p.cap_tokens = a->table_width * a->block_size;
+  p.num_heads = a->num_heads;
+  p.num_kv_heads = a->num_kv_heads;
+  p.heads_per_kv = a->num_heads / a->num_kv_heads;
+  p.head_dim = a->head_dim;
+  p.block_size = a->block_size;
+  p.bs_shift = (a->block_size & (a->block_size - 1)) == 0 ? __builtin_ctz((unsigned)a->block_size) : -1;
+  p.table_i64 = a->table_type == IKL_I64;
+  p.idx_i64 = a->lens_type == IKL_I64;
+  const float scale = a->scale > 0.f ? a->scale : 1.f / sqrtf((float)a->head_dim);
+  p.scale_log2 = scale * LOG2E;
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipEvent_t ev0 = static_cast<hipEvent_t>(a->events[0]), ev1 = static_cast<hipEvent_t>(a->events[1]);
+  if (ev0 && hipEventRecord(ev0, s) != hipSuccess) return check_launch("ikl_paged_prefill_attention: event record");
+  hipError_t err;
+  if (path == IKL_PATH_MFMA_GROUPED) {
+    constexpr int NG = IKL_PREFILL_NG;
+    const int64_t rows = a->query_width * p.heads_per_kv;
+    constexpr int64_t rows_per_wg = 16 * NG * PWAVES;  // RWG of the kernel
+    p.row_blocks = (rows + rows_per_wg - 1) / rows_per_wg;
+    p.bh_pad = (a->batch * a->num_kv_heads + 7) / 8 * 8;
+    const int64_t blocks = p.row_blocks * p.bh_pad;
+    if (blocks > 0x7fffffffLL) return fail(IKL_EINVAL, "ikl_paged_prefill_attention: launch too large");
+    const dim3 grid((unsigned)blocks);
+    if (a->dtype == IKL_BF16) err = launch_mfma_dim<bf16_tag, NG>(a->head_dim, p, grid, s);
+    else err = launch_mfma_dim<f16_tag, NG>(a->head_dim, p, grid, s);
+  } else {
+    const int64_t blocks = a->batch * a->num_heads * a->query_width;
+    if (blocks > 0x7fffffffLL) return fail(IKL_EINVAL, "ikl_paged_prefill_attention: launch too large");
+    const dim3 grid((unsigned)blocks);
+    if (a->dtype == IKL_BF16) paged_prefill_scalar_kernel<bf16_tag><<<grid, 64, 0, s>>>(p);
+    else if (a->dtype == IKL_F16) paged_prefill_scalar_kernel<f16_tag><<<grid, 64, 0, s>>>(p);
+    else paged_prefill_scalar_kernel<f32_tag><<<grid, 64, 0, s>>>(p);
+    err = hipGetLastError();
+  }
+  if (err != hipSuccess) return fail(IKL_ELAUNCH, std::string("ikl_paged_prefill_attention: ") + hipGetErrorString(err));
+  if (ev1 && hipEventRecord(ev1, s) != hipSuccess) return check_launch("ikl_paged_prefill_attention: event record");
+  return IKL_OK;
+}

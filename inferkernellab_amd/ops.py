@@ -8,6 +8,9 @@ reference's Triton operators:
 * :func:`paged_decode_attention_hip_grouped` —
   ``paged_decode_attention_triton_grouped`` (triton_ops.py:481-610);
 * :func:`append_kv_hip` — ``append_kv_triton`` (append.py:69-106);
+* :func:`paged_prefill_attention_hip` — ``paged_prefill_attention_sdpa``
+  (attention.py:230-321), one kernel over the paged cache instead of the
+  gather + masked SDPA;
 * :func:`paged_decode_grouped_path` — ``paged_decode_grouped_path``
   (triton_ops.py:56-75), answering with this library's kernel families;
 * :func:`hip_available` / :func:`hip_append_available` —
@@ -615,6 +618,190 @@ class PreparedAppend:
         stream = torch.cuda.current_stream(self.device).cuda_stream
         status = self._lib.ikl_append_kv(ctypes.byref(self._args), ctypes.c_void_p(stream))
         _lib.check(status, "append_kv")
+
+
+# ------------------------------------------------------------ prefill
+def paged_prefill_path(*, dtype: torch.dtype, head_dim: int, block_size: int = 16) -> str:
+    """Kernel family of a prefill launch: ``"mfma_grouped"`` for fp16/bf16
+    with head_dim in {32, 64, 96, 128} and a block size that is a multiple
+    of 16, else ``"scalar_grouped"``. Same rule as the library's
+    ``ikl_paged_prefill_path``."""
+    if (
+        dtype in (torch.float16, torch.bfloat16)
+        and head_dim in (32, 64, 96, 128)
+        and block_size > 0
+        and block_size % 16 == 0
+    ):
+        return "mfma_grouped"
+    return "scalar_grouped"
+
+
+def _prefill_ranges(query_starts, context_lens, batch: int, query_width: int) -> tuple[list[int], list[int]]:
+    """Host copies of the chunk ranges with the checks of attention.py:257-273."""
+    starts = (
+        query_starts.detach().cpu().tolist() if isinstance(query_starts, torch.Tensor) else list(query_starts)
+    )
+    ends = context_lens.detach().cpu().tolist() if isinstance(context_lens, torch.Tensor) else list(context_lens)
+    if len(starts) != batch or len(ends) != batch:
+        raise ValueError("query_starts and context_lens must have one entry per query batch")
+    spans = [int(e) - int(s) for s, e in zip(starts, ends)]
+    if any(int(s) < 0 or n <= 0 for s, n in zip(starts, spans)):
+        raise ValueError("prefill ranges must be non-empty and non-negative")
+    if max(spans) > query_width:
+        raise ValueError("query width is smaller than a prefill range")
+    return [int(s) for s in starts], [int(e) for e in ends]
+
+
+def _prefill_table(block_tables, cache, batch: int, ends: list[int]) -> torch.Tensor:
+    """Block table on the cache device with the checks of attention.py:275-288."""
+    if isinstance(block_tables, torch.Tensor):
+        dtype = block_tables.dtype if block_tables.dtype in _INDEX_TYPES else torch.int64
+        table = block_tables.to(device=cache.device, dtype=dtype)
+    else:
+        table = torch.as_tensor(block_tables, dtype=torch.int32, device=cache.device)
+    if table.ndim != 2 or table.shape[0] != batch:
+        raise ValueError("block_tables must have one row per query batch")
+    max_context = max(ends)
+    if max_context <= 0:
+        raise ValueError("context lengths must be positive")
+    bs = cache.layout.block_size
+    if (max_context + bs - 1) // bs > table.shape[1]:
+        raise ValueError("context length exceeds block table capacity")
+    return table if table.stride(-1) == 1 else table.contiguous()
+
+
+def _aligned_prefill_rows(t: torch.Tensor, width: int) -> bool:
+    vec = max(1, width // t.element_size())
+    return t.data_ptr() % width == 0 and all(s % vec == 0 for s in t.stride()[:-1]) and t.stride(-1) == 1
+
+
+class PreparedPagedPrefill:
+    """Paged prefill attention for one batch of prompt chunks, checked once.
+
+    Binds the cache, the block tables and the chunk ranges (row ``t`` of
+    request ``b`` sits at position ``query_starts[b] + t``; the chunk ends at
+    ``context_lens[b]``); each call takes one layer's query ``[B, H, T, D]``
+    and enqueues one kernel on the current stream, so a layer loop pays the
+    range checks and the host-to-device copy of the ranges once. Results
+    equal :func:`paged_prefill_attention_hip`.
+    """
+
+    def __init__(self, cache, block_tables, query_starts, context_lens, *, num_heads: int,
+                 query_width: int, scale: float | None = None, path: str | None = None):
+        layout = cache.layout
+        if num_heads <= 0 or num_heads % layout.num_kv_heads != 0:
+            raise ValueError("num_heads must be divisible by num_kv_heads")
+        batch = len(query_starts)
+        self.starts, self.ends = _prefill_ranges(query_starts, context_lens, batch, query_width)
+        self.block_tables = _prefill_table(block_tables, cache, batch, self.ends)
+        if cache.dtype not in _DTYPES:
+            raise ValueError("cache dtype must be float16, bfloat16 or float32")
+        self.path = path or paged_prefill_path(dtype=cache.dtype, head_dim=layout.head_dim,
+                                               block_size=layout.block_size)
+        if self.path not in ("mfma_grouped", "scalar_grouped"):
+            raise ValueError("path must be 'mfma_grouped' or 'scalar_grouped'")
+        self._row_align = 16 if self.path == "mfma_grouped" else 4
+        for tensor in (cache.k, cache.v):
+            if not _aligned_prefill_rows(tensor, self._row_align):
+                raise ValueError("cache tensors must have aligned head_dim rows")
+        self._lib = _require_backend()
+        self.cache = cache
+        self.shape = (batch, num_heads, query_width, layout.head_dim)
+        ranges = torch.tensor([self.starts, self.ends], dtype=torch.int32)
+        self.ranges = ranges.to(cache.device, non_blocking=False)
+        a = _lib.PagedPrefillArgs()
+        a.block_tables = self.block_tables.data_ptr()
+        a.table_type = _INDEX_TYPES[self.block_tables.dtype]
+        a.table_stride_b = self.block_tables.stride(0)
+        a.table_width = self.block_tables.shape[1]
+        a.query_starts = self.ranges[0].data_ptr()
+        a.context_lens = self.ranges[1].data_ptr()
+        a.lens_type = _lib.IKL_I32
+        a.batch, a.query_width = batch, query_width
+        a.num_blocks = layout.num_blocks
+        a.num_heads, a.num_kv_heads = num_heads, layout.num_kv_heads
+        a.head_dim, a.block_size = layout.head_dim, layout.block_size
+        a.dtype = _DTYPES[cache.dtype]
+        a.scale = float(scale if scale is not None else layout.head_dim**-0.5)
+        a.path = _PATH_IDS[self.path]
+        self._args = a
+
+    def kernel_name(self) -> str:
+        return "paged_prefill_mfma_kernel" if self.path == "mfma_grouped" else "paged_prefill_scalar_kernel"
+
+    def __call__(self, query: torch.Tensor, layer: int = 0, *, out: torch.Tensor | None = None,
+                 events=None) -> torch.Tensor:
+        layout = self.cache.layout
+        if tuple(query.shape) != self.shape:
+            raise ValueError(f"query must have shape {list(self.shape)}")
+        if query.dtype != self.cache.dtype or query.device != self.cache.device:
+            raise ValueError("query and cache must have the same dtype and device")
+        if not 0 <= layer < layout.num_layers:
+            raise IndexError("layer is out of range")
+        if not _aligned_prefill_rows(query, self._row_align):
+            query = query.contiguous()
+        if out is None:
+            out = torch.empty(self.shape, dtype=query.dtype, device=query.device)
+        elif (tuple(out.shape) != self.shape or out.dtype != query.dtype or out.device != query.device
+              or not _aligned_prefill_rows(out, 8 if self.path == "mfma_grouped" else 4)):
+            raise ValueError("out must match the query shape, dtype and device with aligned rows")
+        kc, vc = self.cache.k[layer], self.cache.v[layer]
+        a = self._args
+        a.query = query.data_ptr()
+        a.q_stride_b, a.q_stride_h, a.q_stride_t = query.stride(0), query.stride(1), query.stride(2)
+        a.k_cache, a.v_cache = kc.data_ptr(), vc.data_ptr()
+        a.k_stride_block, a.k_stride_token, a.k_stride_head = kc.stride()[:3]
+        a.v_stride_block, a.v_stride_token, a.v_stride_head = vc.stride()[:3]
+        a.out = out.data_ptr()
+        a.out_stride_b, a.out_stride_h, a.out_stride_t = out.stride(0), out.stride(1), out.stride(2)
+        for i in range(2):
+            a.events[i] = events[i] if events is not None else None
+        with torch.cuda.device(query.device):
+            stream = torch.cuda.current_stream(query.device).cuda_stream
+            status = self._lib.ikl_paged_prefill_attention(ctypes.byref(a), ctypes.c_void_p(stream))
+        _lib.check(status, "paged prefill attention")
+        return out
+
+
+def paged_prefill_attention_hip(
+    query: torch.Tensor,
+    cache,
+    block_tables,
+    query_starts,
+    context_lens,
+    *,
+    scale: float | None = None,
+    layer: int = 0,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Causal attention of a ragged prefill batch over the paged cache.
+
+    Arguments, checks (same order and messages) and result of
+    ``paged_prefill_attention_sdpa`` (attention.py:230-321): ``query`` is
+    ``[B, H, T, D]``; row ``t`` of request ``b`` sits at position
+    ``query_starts[b] + t`` and attends positions up to its own inside
+    ``[0, context_lens[b])``; rows past ``context_lens[b] - query_starts[b]``
+    are padding and receive the value at position 0, as the reference's mask
+    leaves them. The cache must already hold the chunk's keys and values.
+    One HIP kernel reads K/V straight from the paged cache — no gathered
+    copy of the prefix is made.
+    """
+    if query.ndim != 4:
+        raise ValueError("query must be [B,H,T,D]")
+    batch, num_heads, query_width, head_dim = query.shape
+    layout = cache.layout
+    if head_dim != layout.head_dim:
+        raise ValueError("query head_dim does not match cache")
+    if num_heads % layout.num_kv_heads != 0:
+        raise ValueError("num_heads must be divisible by num_kv_heads")
+    if query.device != cache.device:
+        raise ValueError("query and cache must be on the same device")
+    starts, ends = _prefill_ranges(query_starts, context_lens, batch, query_width)
+    if not 0 <= layer < layout.num_layers:
+        raise IndexError("layer is out of range")
+    prepared = PreparedPagedPrefill(cache, block_tables, starts, ends, num_heads=num_heads,
+                                    query_width=query_width, scale=scale)
+    return prepared(query, layer, out=out)
 
 
 # Names of the reference's operators, bound to the same HIP functions.

@@ -15,6 +15,8 @@ It restates, in numpy, the reference's algorithm for this path:
 * ``dense_decode_attention``     — attention.py:18-36 (fp32 einsum/softmax/einsum)
 * ``paged_decode_attention``     — attention.py:134-175 (= backend ``paged_reference``)
 * ``rope_rows``                  — hf_benchmark.py:69-85 (rotate-half RoPE before the append)
+* ``paged_prefill_attention``    — attention.py:230-321 (gather + causal masked SDPA of a
+  ragged prompt-chunk batch)
 
 Storage keeps the cache's own element type: float16 and float32 as numpy
 arrays of that type, bfloat16 as raw ``uint16`` bit patterns (numpy has no
@@ -32,7 +34,12 @@ Parity pins (each checked in tests/test_oracle.py):
   explicit head expansion, block-table permutation invariance, and torch's
   own softmax/einsum on the same data;
 * rope_rows: torch's own elementwise ops on the same storage, bit for bit,
-  in the three dtypes; position 0 (cos 1, sin 0) is the identity.
+  in the three dtypes; position 0 (cos 1, sin 0) is the identity;
+* paged_prefill_attention: every attending row equals the (pinned) decode
+  attention over its own prefix — the check of the reference's test
+  (tests/test_attention.py:90-116), run on that test's tables and ranges —
+  plus a float64 causal brute force and torch SDPA under the reference's
+  mask construction (padding rows included).
 """
 
 from __future__ import annotations
@@ -247,4 +254,72 @@ def brute_force_attention_f64(query, keys, values, *, scale=None):
         z = sum(weights)
         out.append([sum(weights[t] * values[t][kvh][d] for t in range(len(keys))) / z
                     for d in range(head_dim)])
+    return out
+
+
+def causal_allow(positions: np.ndarray, num_keys: int) -> np.ndarray:
+    """[n, num_keys] mask: the row at position p may attend keys 0..p
+    (attention.py:301-303)."""
+    return np.arange(num_keys)[None, :] <= np.asarray(positions)[:, None]
+
+
+def paged_prefill_attention(query_f32: np.ndarray, cache: OracleCache, block_tables, query_starts,
+                            context_lens, *, scale: float | None = None, layer: int = 0) -> np.ndarray:
+    """Causal attention of a ragged prompt-chunk batch (attention.py:230-321).
+
+    ``query_f32`` is [B, H, T, D]; row t of request b sits at position
+    starts[b] + t. Rows t < ends[b] - starts[b] attend positions
+    [0, starts[b] + t] in fp32; the remaining (padding) rows are allowed only
+    position 0 by the reference's mask (attention.py:305), so they equal the
+    value there. Returns fp32 [B, H, T, D].
+    """
+    q = np.asarray(query_f32, dtype=np.float32)
+    if q.ndim != 4:
+        raise ValueError("query must be [B,H,T,D]")
+    batch, num_heads, width, head_dim = q.shape
+    if head_dim != cache.head_dim:
+        raise ValueError("query head_dim does not match cache")
+    if num_heads % cache.num_kv_heads != 0:
+        raise ValueError("num_heads must be divisible by num_kv_heads")
+    starts = [int(x) for x in np.asarray(query_starts).reshape(-1)]
+    ends = [int(x) for x in np.asarray(context_lens).reshape(-1)]
+    tables = [list(map(int, row)) for row in block_tables]
+    if len(starts) != batch or len(ends) != batch:
+        raise ValueError("query_starts and context_lens must have one entry per query batch")
+    spans = [e - s for s, e in zip(starts, ends)]
+    if any(s < 0 or n <= 0 for s, n in zip(starts, spans)):
+        raise ValueError("prefill ranges must be non-empty and non-negative")
+    if max(spans) > width:
+        raise ValueError("query width is smaller than a prefill range")
+    sc = np.float32(scale if scale is not None else head_dim ** -0.5)
+    out = np.empty(q.shape, dtype=np.float32)
+    for b in range(batch):
+        k_raw, v_raw = cache.read(layer, tables[b], ends[b])
+        k = expand_kv(to_f32(k_raw, cache.dtype), num_heads).transpose(1, 0, 2)  # [H, L, D]
+        v = expand_kv(to_f32(v_raw, cache.dtype), num_heads).transpose(1, 0, 2)
+        n = spans[b]
+        scores = np.matmul(q[b, :, :n], k.transpose(0, 2, 1)) * sc  # [H, n, L]
+        allow = causal_allow(starts[b] + np.arange(n), ends[b])  # [n, L]
+        scores = np.where(allow[None], scores, -np.inf).astype(np.float32)
+        scores -= scores.max(axis=-1, keepdims=True)
+        probs = np.exp(scores, dtype=np.float32)
+        probs /= probs.sum(axis=-1, keepdims=True)
+        out[b, :, :n] = np.matmul(probs, v)
+        out[b, :, n:] = v[:, :1, :]  # padding rows: position 0
+    return out
+
+
+def brute_force_prefill_f64(query, keys, values, start: int, *, scale=None):
+    """Pure-Python float64 causal attention for tiny inputs: query [H][n][D]
+    (row t at position start + t), keys/values [L][Hkv][D]; returns [H][n][D]."""
+    out = []
+    for h in range(len(query)):
+        rows = []
+        for t, qrow in enumerate(query[h]):
+            pos = start + t
+            rows.append(brute_force_attention_f64([qrow], [[kv[h * len(keys[0]) // len(query)]]
+                                                           for kv in keys[: pos + 1]],
+                                                  [[vv[h * len(values[0]) // len(query)]]
+                                                   for vv in values[: pos + 1]], scale=scale)[0])
+        out.append(rows)
     return out

@@ -132,3 +132,57 @@ def make_case(
 def max_abs_err(actual: torch.Tensor, expected: np.ndarray) -> float:
     a = actual.detach().float().cpu().numpy()
     return float(np.max(np.abs(a - expected)))
+
+
+@dataclass
+class PrefillCase:
+    """A ragged prompt-chunk batch: request b's chunk covers positions
+    [starts[b], ends[b]) of a context already written up to ends[b]."""
+
+    base: Case
+    query: np.ndarray  # storage [B, H, T, D]
+    starts: list[int]
+    ends: list[int]
+
+    @property
+    def dtype(self) -> str:
+        return self.base.dtype
+
+    @property
+    def query_f32(self) -> np.ndarray:
+        return po.to_f32(self.query, self.dtype)
+
+    def expected(self, scale=None, layer=0) -> np.ndarray:
+        return po.paged_prefill_attention(self.query_f32, self.base.oracle_cache, self.base.tables,
+                                          self.starts, self.ends, scale=scale, layer=layer)
+
+    def device_query(self, device="cuda") -> torch.Tensor:
+        return storage_to_torch(self.query, self.dtype).to(device)
+
+
+def make_prefill_case(*, starts, ends, width: int | None = None, num_heads: int, num_kv_heads: int,
+                      head_dim: int, block_size: int, dtype: str, seed: int = 0, num_layers: int = 1,
+                      layer: int = 0, table_slack: int = 0) -> PrefillCase:
+    """make_case() with context lengths `ends`, plus a seeded [B, H, T, D]
+    query whose width T defaults to the longest chunk. `table_slack` extra
+    blocks of context room are allocated per request (unwritten, NaN)."""
+    ends = [int(e) for e in ends]
+    starts = [int(s) for s in starts]
+    base = make_case(batch=len(ends), num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim,
+                     block_size=block_size, lengths=[e + table_slack * block_size for e in ends],
+                     dtype=dtype, seed=seed, num_layers=num_layers, layer=layer)
+    # positions past ends[b] stay mapped by the table but must never be
+    # attended: poison them with NaN
+    oc = base.oracle_cache
+    nan = np.uint16(0x7FC0) if dtype == "bfloat16" else np.nan
+    for table, e in zip(base.tables, ends):
+        total = len(table) * block_size
+        if total > e:
+            slots = oc.slot_mapping(table, e, total - e)
+            oc.k[layer, slots // block_size, slots % block_size] = nan
+            oc.v[layer, slots // block_size, slots % block_size] = nan
+    base.lengths = ends
+    width = width or max(e - s for s, e in zip(starts, ends))
+    gen = torch.Generator().manual_seed(seed + 7919)
+    query = randn_storage(gen, (len(ends), num_heads, width, head_dim), dtype)
+    return PrefillCase(base, query, starts, ends)

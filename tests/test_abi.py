@@ -36,6 +36,7 @@ def test_struct_layouts_match_header_field_order():
     for struct_name, cls in (("ikl_append_args", _lib.AppendArgs),
                              ("ikl_paged_attention_args", _lib.PagedAttentionArgs),
                              ("ikl_rope_append_args", _lib.RopeAppendArgs),
+                             ("ikl_paged_prefill_args", _lib.PagedPrefillArgs),
                              ("ikl_launch_config", _lib.LaunchConfig)):
         body = re.search(r"typedef struct %s \{(.*?)\}" % struct_name, text, flags=re.S).group(1)
         fields = []
@@ -199,3 +200,90 @@ def test_rope_append_rejects_bad_arguments_without_a_gpu():
     assert "null tensor" in _lib.last_error()
     a.num_tokens = 0
     assert lib.ikl_rope_append_kv(ctypes.byref(a), None) == _lib.IKL_OK  # nothing to do
+
+
+@pytest.mark.parametrize(
+    ("dtype", "head_dim", "block_size", "expected"),
+    [
+        (torch.bfloat16, 128, 16, "mfma_grouped"),
+        (torch.float16, 96, 48, "mfma_grouped"),
+        (torch.bfloat16, 32, 32, "mfma_grouped"),
+        (torch.float32, 128, 16, "scalar_grouped"),
+        (torch.bfloat16, 128, 8, "scalar_grouped"),
+        (torch.float16, 256, 16, "scalar_grouped"),
+        (torch.bfloat16, 80, 16, "scalar_grouped"),
+    ],
+)
+def test_prefill_path_truth_table_matches_library(dtype, head_dim, block_size, expected):
+    assert ops.paged_prefill_path(dtype=dtype, head_dim=head_dim, block_size=block_size) == expected
+    code = _lib.load().ikl_paged_prefill_path(ops._DTYPES[dtype], head_dim, block_size)
+    assert ops._PATH_NAMES[code] == expected
+
+
+def _prefill_args(**kw):
+    a = _lib.PagedPrefillArgs()
+    a.batch, a.query_width, a.num_heads, a.num_kv_heads, a.head_dim = 2, 64, 32, 8, 128
+    a.block_size, a.num_blocks, a.table_width = 16, 100, 8
+    a.table_type = a.lens_type = _lib.IKL_I32
+    a.dtype = _lib.IKL_BF16
+    a.path = -1
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_prefill_entry_rejects_bad_arguments_before_any_launch():
+    """Every check below returns before the library touches a device."""
+    lib = _lib.load()
+    assert lib.ikl_paged_prefill_attention(None, None) == _lib.IKL_EINVAL
+    a = _prefill_args(num_heads=30)
+    assert lib.ikl_paged_prefill_attention(ctypes.byref(a), None) == _lib.IKL_EINVAL
+    assert "sizes must be positive" in _lib.last_error() or "divisible" in _lib.last_error()
+    a = _prefill_args(query_width=0)
+    assert lib.ikl_paged_prefill_attention(ctypes.byref(a), None) == _lib.IKL_EINVAL
+    assert "positive" in _lib.last_error()
+    a = _prefill_args()  # NULL tensors
+    assert lib.ikl_paged_prefill_attention(ctypes.byref(a), None) == _lib.IKL_EINVAL
+    assert "NULL" in _lib.last_error()
+    fake = 1 << 20  # never dereferenced: the checks below fail first
+    ptrs = dict(query=fake, k_cache=fake, v_cache=fake, block_tables=fake, query_starts=fake,
+                context_lens=fake, out=fake)
+    a = _prefill_args(dtype=_lib.IKL_F32, head_dim=512, **ptrs)
+    assert lib.ikl_paged_prefill_attention(ctypes.byref(a), None) == _lib.IKL_EUNSUPPORTED
+    a = _prefill_args(dtype=_lib.IKL_F32, path=_lib.IKL_PATH_MFMA_GROUPED, **ptrs)
+    assert lib.ikl_paged_prefill_attention(ctypes.byref(a), None) == _lib.IKL_EUNSUPPORTED
+    assert "no MFMA kernel" in _lib.last_error()
+    a = _prefill_args(path=7, **ptrs)
+    assert lib.ikl_paged_prefill_attention(ctypes.byref(a), None) == _lib.IKL_EINVAL
+    a = _prefill_args(q_stride_t=100, **ptrs)  # 200-byte rows: not 16-byte aligned
+    assert lib.ikl_paged_prefill_attention(ctypes.byref(a), None) == _lib.IKL_EINVAL
+    assert "misaligned" in _lib.last_error()
+
+
+@pytest.mark.parametrize(
+    ("shape", "tables", "starts", "ends", "layer", "error", "message"),
+    [
+        ((2, 4, 8), [[0], [1]], [0, 0], [4, 4], 0, ValueError, r"query must be \[B,H,T,D\]"),
+        ((2, 4, 8, 32), [[0], [1]], [0, 0], [4, 4], 0, ValueError, "head_dim does not match"),
+        ((2, 3, 8, 16), [[0], [1]], [0, 0], [4, 4], 0, ValueError, "divisible by num_kv_heads"),
+        ((2, 4, 8, 16), [[0], [1]], [0], [4, 4], 0, ValueError, "one entry per query batch"),
+        ((2, 4, 8, 16), [[0], [1]], [0, 4], [4, 4], 0, ValueError, "non-empty and non-negative"),
+        ((2, 4, 8, 16), [[0], [1]], [-1, 0], [4, 4], 0, ValueError, "non-empty and non-negative"),
+        ((2, 4, 8, 16), [[0, 1], [2, 3]], [0, 0], [9, 4], 0, ValueError, "query width is smaller"),
+        ((2, 4, 8, 16), [[0], [1]], [0, 0], [4, 4], 2, IndexError, "layer is out of range"),
+        ((2, 4, 8, 16), [[0]], [0, 0], [4, 4], 0, ValueError, "one row per query batch"),
+        ((2, 4, 8, 16), [[0], [1]], [0, 0], [5, 4], 0, ValueError, "exceeds block table capacity"),
+        ((2, 4, 8, 16), [[0], [1]], [0, 0], [4, 4], 0, RuntimeError, "unavailable"),
+    ],
+)
+def test_prefill_operator_checks_in_the_reference_order(shape, tables, starts, ends, layer, error, message):
+    """attention.py:252-288's checks (same order, same messages); a valid
+    call on a host without a GPU fails loudly instead of computing."""
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    from inferkernellab_amd import PagedKVCache
+
+    cache = PagedKVCache(8, 4, 2, 16, dtype=torch.bfloat16)
+    q = torch.zeros(shape, dtype=torch.bfloat16)
+    with pytest.raises(error, match=message):
+        ops.paged_prefill_attention_hip(q, cache, tables, starts, ends, layer=layer)
