@@ -19,6 +19,12 @@ divided by its wall time (GB/s); ``roofline`` times the attention partition
 kernel with HIP events recorded around it on its stream; ``cpu_baseline``
 times the CPU oracle (a numpy restatement of paged_reference) on a bounded
 sample of the same requests.
+
+``--workload prefill_*`` measures the paged prefill attention kernel
+instead (one causal launch over a batch of prompt chunks): ``value`` and
+``roofline`` in TFLOP/s of algorithmic flops against the dense bf16 MFMA
+peak, with the reference's gather + masked SDPA path timed on the same GPU
+beside it.
 """
 
 from __future__ import annotations
@@ -189,12 +195,234 @@ def cpu_baseline(w, budget_s: float) -> dict:
     }
 
 
+# ------------------------------------------------------------------ prefill
+PEAK_MFMA_TFLOPS = 2500.0  # MI355X dense bf16 / fp16 matrix peak
+PREFILL_METRIC = "paged prefill attention TFLOP/s (causal, algorithmic flops), bf16"
+PREFILL_WORKLOADS = {
+    # name: (batch, heads, kv_heads, head_dim, dtype, chunk start, chunk end) — every request
+    # runs the chunk [start, end) of a prompt whose positions [0, start) are already cached
+    "prefill_gqa32x8_hd128_bf16_b8_4k": (8, 32, 8, 128, torch.bfloat16, 0, 4096),
+    "prefill_chunk_gqa32x8_hd128_bf16_b8_3k+1k": (8, 32, 8, 128, torch.bfloat16, 3072, 4096),
+    "prefill_gqa16x4_hd128_bf16_b8_512": (8, 16, 4, 128, torch.bfloat16, 0, 512),
+}
+
+
+def build_prefill_workload(name: str, device: torch.device, seed: int = 0):
+    from inferkernellab_amd import PagedKVCache
+
+    batch, heads, kv_heads, head_dim, dtype, start, end = PREFILL_WORKLOADS[name]
+    block_size = 16
+    gen = torch.Generator().manual_seed(seed)
+    need = -(-end // block_size)
+    pool = batch * need + 8
+    perm = torch.randperm(pool, generator=gen).tolist()
+    tables = [perm[b * need : (b + 1) * need] for b in range(batch)]
+    cache = PagedKVCache(pool, block_size, kv_heads, head_dim, dtype=dtype, device=device)
+    dgen = torch.Generator(device=device).manual_seed(seed + 1)
+    for t in (cache.k, cache.v):
+        t.normal_(0.0, 1.0, generator=dgen)
+    width = end - start
+    query = torch.randn(batch, heads, width, head_dim, generator=dgen, device=device).to(dtype)
+    return {
+        "cache": cache, "query": query, "tables_list": tables,
+        "tables": torch.tensor(tables, dtype=torch.int32, device=device),
+        "starts": [start] * batch, "ends": [end] * batch, "dtype": dtype, "heads": heads,
+        "kv_heads": kv_heads, "head_dim": head_dim, "block_size": block_size, "pool": pool,
+    }
+
+
+def prefill_pairs(starts, ends) -> int:
+    """Attended (query row, key) pairs per head: row t of a chunk [s, e) sees s + t + 1 keys."""
+    return sum((e - s) * s + (e - s) * (e - s + 1) // 2 for s, e in zip(starts, ends))
+
+
+def prefill_flops(w) -> int:
+    """Algorithmic flops of one prefill attention launch: QK^T and PV, 2 * head_dim
+    each per attended (row, key) pair and query head."""
+    return prefill_pairs(w["starts"], w["ends"]) * w["heads"] * 4 * w["head_dim"]
+
+
+def torch_gather_sdpa(w):
+    """The reference's prefill path restated on the same GPU (attention.py:289-321):
+    gather the whole prefix through the block table, zero the unread slots,
+    build the boolean causal mask and call torch SDPA."""
+    import torch.nn.functional as F
+
+    cache, q = w["cache"], w["query"]
+    bs = w["block_size"]
+    span = max(w["ends"])
+    kpos = torch.arange(span, device=q.device)
+    phys = w["tables"].long()[:, kpos // bs]
+    key = cache.k[0][phys, (kpos % bs).unsqueeze(0)]
+    value = cache.v[0][phys, (kpos % bs).unsqueeze(0)]
+    lengths = torch.tensor(w["ends"], device=q.device).view(-1, 1, 1)
+    starts = torch.tensor(w["starts"], device=q.device).view(-1, 1, 1)
+    key_ok = kpos.view(1, 1, -1) < lengths
+    valid = key_ok.squeeze(1).unsqueeze(-1).unsqueeze(-1)
+    key = key.masked_fill(~valid, 0)
+    value = value.masked_fill(~valid, 0)
+    qpos = torch.arange(q.shape[2], device=q.device)
+    valid_query = qpos.view(1, -1, 1) < (lengths - starts).view(-1, 1, 1)
+    allow = (valid_query & key_ok & (kpos.view(1, 1, -1) <= starts + qpos.view(1, -1, 1))) | (
+        (~valid_query) & (kpos.view(1, 1, -1) == 0))
+    return F.scaled_dot_product_attention(q, key.permute(0, 2, 1, 3), value.permute(0, 2, 1, 3),
+                                          attn_mask=allow.unsqueeze(1), enable_gqa=True)
+
+
+def prefill_cpu_baseline(w, budget_s: float) -> dict:
+    """Times the CPU oracle's paged_prefill_attention on 256-row slices of the
+    workload's chunks (cycling through requests and slices) for ~budget_s,
+    then scales per attended (row, key) pair to the whole launch."""
+    import numpy as np
+    from oracle import paged_oracle as po
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([info.get("num_threads", 1) for info in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    dtype = {torch.bfloat16: "bfloat16", torch.float16: "float16"}[w["dtype"]]
+    oc = po.OracleCache.__new__(po.OracleCache)
+    oc.num_layers, oc.num_blocks, oc.block_size = 1, w["pool"], w["block_size"]
+    oc.num_kv_heads, oc.head_dim, oc.dtype = w["kv_heads"], w["head_dim"], dtype
+
+    def host(t):
+        return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+    oc.k, oc.v = host(w["cache"].k), host(w["cache"].v)
+    q = po.to_f32(host(w["query"]), dtype)
+    batch, width = q.shape[0], q.shape[2]
+    rows = min(256, width)
+    slices = [(b, r0) for r0 in range(0, width, rows) for b in range(batch)]
+    done, elapsed, pairs = 0, 0.0, 0
+    while elapsed < budget_s and done < 4 * len(slices):
+        b, r0 = slices[(len(slices) - 1 - done) % len(slices)]  # longest rows first
+        s = w["starts"][b] + r0
+        e = min(s + rows, w["ends"][b])
+        t0 = time.perf_counter()
+        po.paged_prefill_attention(q[b : b + 1, :, r0 : r0 + (e - s)], oc, [w["tables_list"][b]], [s], [e])
+        elapsed += time.perf_counter() - t0
+        pairs += prefill_pairs([s], [e])
+        done += 1
+    step_s = elapsed / pairs * prefill_pairs(w["starts"], w["ends"])
+    return {
+        "value": round(step_s * 1e6, 1),
+        "unit": "us/step",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle paged_prefill_attention (numpy fp32), {done} slices of <= {rows} rows "
+                  f"({pairs} attended row-key pairs per head, {elapsed:.1f} s), scaled per attended "
+                  f"pair to the full launch",
+    }
+
+
+def run_prefill(args, device) -> int:
+    from inferkernellab_amd import PreparedPagedPrefill
+
+    w = build_prefill_workload(args.workload, device, args.seed)
+    q = w["query"]
+    prep = PreparedPagedPrefill(w["cache"], w["tables"], w["starts"], w["ends"], num_heads=w["heads"],
+                                query_width=q.shape[2])
+    out = torch.empty_like(q)
+    events = HipEvents()
+    k_steps, warmup = args.steps, args.warmup
+    ev = [[events.create() for _ in range(2)] for _ in range(k_steps)]
+    for _ in range(warmup):
+        prep(q, 0, out=out)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(k_steps):
+        prep(q, 0, out=out, events=ev[i])
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    kernel_ms = [events.elapsed_ms(e[0], e[1]) for e in ev]
+    for pair in ev:
+        for h in pair:
+            events.destroy(h)
+    flops = prefill_flops(w)
+    ms_per_step = wall_s * 1e3 / k_steps
+    kern_ms = sum(kernel_ms) / len(kernel_ms)
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+
+    # the reference's gather + masked SDPA on the same GPU, for comparison
+    sdpa_ms = None
+    scores_bytes = q.shape[0] * q.shape[1] * q.shape[2] * max(w["ends"]) * 4
+    if scores_bytes < (48 << 30):
+        ref = torch_gather_sdpa(w)
+        err = float((ref.float() - out.float()).abs().max())
+        del ref
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(3):
+            torch_gather_sdpa(w)
+        stop.record()
+        torch.cuda.synchronize()
+        sdpa_ms = start.elapsed_time(stop) / 3
+    else:
+        err = None
+
+    traffic = None
+    traffic_file = ROOT / "profiles" / f"traffic_{args.workload}.json"
+    if traffic_file.exists():
+        try:
+            traffic = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    cpu = None if args.no_cpu_baseline else prefill_cpu_baseline(w, args.cpu_budget_s)
+    value = flops / (ms_per_step * 1e-3) / 1e12
+    record = {
+        "metric": PREFILL_METRIC,
+        "value": round(value, 1),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": k_steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "us_per_step": round(ms_per_step * 1e3, 1),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16"}[w["dtype"]],
+        "data": "synthetic (seeded N(0,1) K/V/q, random-permutation block tables)",
+        "config": {
+            "workload": args.workload,
+            "batch": q.shape[0],
+            "num_heads": w["heads"],
+            "num_kv_heads": w["kv_heads"],
+            "head_dim": w["head_dim"],
+            "block_size": w["block_size"],
+            "chunk": [w["starts"][0], w["ends"][0]],
+            "step": "one paged prefill attention launch over the batch's chunks (causal)",
+            "parallelism": "single GPU",
+        },
+        "prefill_kernel_us": round(kern_ms * 1e3, 2),
+        "algorithmic_flops_per_launch": flops,
+        "torch_gather_sdpa_us": round(sdpa_ms * 1e3, 1) if sdpa_ms is not None else None,
+        "max_abs_diff_vs_torch_sdpa": err,
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_MFMA_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_MFMA_TFLOPS, 4),
+            "traffic": traffic,
+            "kernel": prep.kernel_name(),
+            "algorithmic_flops_per_launch": flops,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(record))
+    return 0
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=10)
-    parser.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
+    parser.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS))
     parser.add_argument("--partition-size", type=int, default=None,
                         help="tokens per fixed split partition (default: the library's automatic split)")
     parser.add_argument("--cpu-budget-s", type=float, default=15.0)
@@ -226,6 +454,9 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration": {"bytes_read": nbytes, "bytes_written": nbytes, "launches": 3}}))
         return 0
+
+    if args.workload in PREFILL_WORKLOADS:
+        return run_prefill(args, device)
 
     from inferkernellab_amd import ops
 

@@ -44,6 +44,12 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source additions. The prefill kernels produce no NaN of their own
+# (masked scores are -inf, never 0/0): without NaN handling, fmaxf skips the
+# IEEE canonicalisation of its operands in the softmax.
+SOURCE_FLAGS = {"paged_prefill.hip": ["-fno-honor-nans"]}
+
+
 def _hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(path).exists():
@@ -67,7 +73,8 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
     jobs = min(len(SOURCES), max(1, os.cpu_count() or 1))
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
         futures = [
-            pool.submit(_compile, hipcc, CSRC / name, obj, extra) for name, obj in zip(SOURCES, objs)
+            pool.submit(_compile, hipcc, CSRC / name, obj, [*SOURCE_FLAGS.get(name, []), *extra])
+            for name, obj in zip(SOURCES, objs)
         ]
         for future in futures:
             future.result()

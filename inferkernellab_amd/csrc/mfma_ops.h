@@ -49,6 +49,7 @@ struct mfma_ops<bf16_tag> {
   __device__ static inline float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
   // A 16-bit P keeps 8 significant bits: worth splitting into two MFMAs.
   static constexpr bool NARROW_P = true;
+  static constexpr uint32_t ONE2 = 0x3f803f80u;  // two 1.0 elements
 };
 
 template <>
@@ -67,6 +68,7 @@ struct mfma_ops<f16_tag> {
   __device__ static inline float lo(uint32_t w) { return (float)__builtin_bit_cast(f16x2_t, w)[0]; }
   __device__ static inline float hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2_t, w)[1]; }
   static constexpr bool NARROW_P = false;  // fp16 P (<= 2^8) already keeps 11 bits
+  static constexpr uint32_t ONE2 = 0x3c003c00u;  // two 1.0 elements
 };
 
 __device__ inline v4u32 zero4() { return v4u32{0u, 0u, 0u, 0u}; }

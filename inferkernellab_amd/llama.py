@@ -217,7 +217,8 @@ class LlamaPagedDecodeRunner:
                  backend: str = "hip_paged_grouped", block_size: int = 16, append_backend: str = "hip",
                  max_num_batched_tokens: int = 2048, prefill_mode: str = "batched",
                  temperature: float = 0.0, top_p: float = 1.0, seed: int = 2026,
-                 eos_token_ids: Sequence[int] | None = None, use_graph: bool = True) -> None:
+                 eos_token_ids: Sequence[int] | None = None, use_graph: bool = True,
+                 prefill_attention: str = "hip") -> None:
         if not prompts:
             raise ValueError("at least one prompt is required")
         if max_new_tokens <= 0:
@@ -230,6 +231,8 @@ class LlamaPagedDecodeRunner:
             raise ValueError(f"unsupported append backend: {append_backend}")
         if prefill_mode not in ("batched", "token"):
             raise ValueError("prefill_mode must be batched or token")
+        if prefill_attention not in ("hip", "torch"):
+            raise ValueError("prefill_attention must be hip or torch")
         if not (math.isfinite(temperature) and temperature >= 0 and math.isfinite(top_p) and 0 < top_p <= 1):
             raise ValueError("temperature must be non-negative and top_p must be in (0, 1]")
         param = next(model.parameters())
@@ -247,6 +250,7 @@ class LlamaPagedDecodeRunner:
             raise ValueError("EOS token id is outside the configured vocabulary")
         ops._require_backend()
         self.backend, self.append_backend, self.prefill_mode = backend, append_backend, prefill_mode
+        self.prefill_attention = prefill_attention
         self.max_new_tokens, self.temperature, self.top_p = max_new_tokens, temperature, top_p
         self._attend = ATTENTION_BACKENDS[backend]
         self.num_layers = int(cfg.num_hidden_layers)
@@ -366,26 +370,56 @@ class LlamaPagedDecodeRunner:
         return out.permute(0, 2, 1, 3).to(q.dtype)
 
     def _forward_prefill(self, token_ids: torch.Tensor, requests, starts, ends) -> torch.Tensor:
-        """Logits [B, T, vocab] of prompt chunks token_ids [B, T] (padded)."""
+        """Logits [B, T, vocab] of prompt chunks token_ids [B, T] (padded).
+
+        With the HIP backends (the default) each layer runs two kernels
+        around its projections: the fused RoPE + append over the batch's
+        tokens (padding rows rotate but are not appended: their slot is -1)
+        and the paged prefill attention (ikl_paged_prefill_attention), which
+        reads the chunk's prefix straight from the cache — the role of
+        paged_prefill_attention_sdpa at hf_benchmark.py:491-498."""
         m = self.model.model
         b, t = token_ids.shape
         spans = [e - s for s, e in zip(starts, ends)]
         hidden = m.embed_tokens(token_ids)
         pos = torch.tensor(list(starts), device=self.device).view(-1, 1) + torch.arange(t, device=self.device)
         cos, sin = m.rotary_emb(hidden, pos)
-        cos, sin = cos.unsqueeze(2), sin.unsqueeze(2)
         tables, _ = self.metadata.for_batch(requests, list(ends))
-        slots = torch.cat([self.cache.slot_mapping(r.block_table, s, n)
-                           for r, s, n in zip(requests, starts, spans)]).to(torch.int32)
+        fused = self.append_backend != "torch"
+        if fused:
+            slot_rows = torch.full((b, t), -1, dtype=torch.int32)
+            for i, (r, s_, n) in enumerate(zip(requests, starts, spans)):
+                slot_rows[i, :n] = torch.as_tensor(self.cache.slot_mapping(r.block_table, s_, n), dtype=torch.int32)
+            slots = slot_rows.reshape(-1).to(self.device)
+            cos2, sin2 = cos.reshape(b * t, self.head_dim).contiguous(), sin.reshape(b * t, self.head_dim).contiguous()
+        else:
+            slots = torch.cat([self.cache.slot_mapping(r.block_table, s_, n)
+                               for r, s_, n in zip(requests, starts, spans)]).to(torch.int32)
+            cos, sin = cos.unsqueeze(2), sin.unsqueeze(2)
+        prefill = None
+        if self.prefill_attention == "hip":
+            prefill = ops.PreparedPagedPrefill(self.cache, tables, list(starts), list(ends),
+                                               num_heads=self.num_heads, query_width=t)
         for li, layer in enumerate(m.layers):
             x = layer.input_layernorm(hidden)
             att = layer.self_attn
-            q = self._rope(att.q_proj(x).view(b, t, self.num_heads, self.head_dim), cos, sin)
-            k = self._rope(att.k_proj(x).view(b, t, self.num_kv_heads, self.head_dim), cos, sin)
+            q = att.q_proj(x).view(b, t, self.num_heads, self.head_dim)
+            k = att.k_proj(x).view(b, t, self.num_kv_heads, self.head_dim)
             v = att.v_proj(x).view(b, t, self.num_kv_heads, self.head_dim)
-            self._append(li, slots, torch.cat([k[i, :n] for i, n in enumerate(spans)]),
-                         torch.cat([v[i, :n] for i, n in enumerate(spans)]))
-            o = self._prefix_attention(q, li, tables, starts, ends)
+            if fused:  # q rotated in place; padding rows of k / v are skipped (slot -1)
+                ops.rope_append_kv_hip(q.view(b * t, self.num_heads, self.head_dim),
+                                       k.reshape(b * t, self.num_kv_heads, self.head_dim),
+                                       v.reshape(b * t, self.num_kv_heads, self.head_dim),
+                                       cos2, sin2, self.cache, slots, layer=li)
+            else:
+                q, k = self._rope(q, cos, sin), self._rope(k, cos, sin)
+                self._append(li, slots, torch.cat([k[i, :n] for i, n in enumerate(spans)]),
+                             torch.cat([v[i, :n] for i, n in enumerate(spans)]))
+            if prefill is not None:
+                o = torch.empty_like(q)  # [B, T, H, D]; the kernel writes its [B, H, T, D] view
+                prefill(q.transpose(1, 2), li, out=o.transpose(1, 2))
+            else:
+                o = self._prefix_attention(q, li, tables, starts, ends)
             hidden = hidden + att.o_proj(o.reshape(b, t, self.num_heads * self.head_dim))
             hidden = self._mlp_residual(layer, hidden)
         return self.model.lm_head(m.norm(hidden))

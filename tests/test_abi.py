@@ -227,6 +227,9 @@ def _prefill_args(**kw):
     a.table_type = a.lens_type = _lib.IKL_I32
     a.dtype = _lib.IKL_BF16
     a.path = -1
+    a.k_stride_block = a.v_stride_block = 16 * 8 * 128
+    a.k_stride_token = a.v_stride_token = 8 * 128
+    a.k_stride_head = a.v_stride_head = 128
     for k, v in kw.items():
         setattr(a, k, v)
     return a
@@ -258,6 +261,12 @@ def test_prefill_entry_rejects_bad_arguments_before_any_launch():
     a = _prefill_args(q_stride_t=100, **ptrs)  # 200-byte rows: not 16-byte aligned
     assert lib.ikl_paged_prefill_attention(ctypes.byref(a), None) == _lib.IKL_EINVAL
     assert "misaligned" in _lib.last_error()
+    a = _prefill_args(k_stride_token=64, **ptrs)  # token rows overlap
+    assert lib.ikl_paged_prefill_attention(ctypes.byref(a), None) == _lib.IKL_EINVAL
+    assert "token strides" in _lib.last_error()
+    a = _prefill_args(table_width=1 << 27, **ptrs)  # positions past 2^31
+    assert lib.ikl_paged_prefill_attention(ctypes.byref(a), None) == _lib.IKL_EINVAL
+    assert "2^31" in _lib.last_error()
 
 
 @pytest.mark.parametrize(

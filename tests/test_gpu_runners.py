@@ -192,6 +192,29 @@ def test_llama_bf16_gqa_hd128_matches_oracle():
     _check_llama(cfg, model, result, prompts, tol=3e-2, margin_check=True)
 
 
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 3e-2)])
+def test_llama_hip_prefill_matches_torch_prefix_attention(dtype, tol):
+    """The batched prefill with ikl_paged_prefill_attention (+ fused RoPE
+    append) against the runner's torch gather + fp32 attention on the same
+    model: chunked prompts (a 48-token budget splits them, so later chunks
+    start past 0) and padding rows."""
+    from inferkernellab_amd.llama import LlamaPagedDecodeRunner
+
+    cfg, model = _llama(dtype, hidden_size=512, intermediate_size=512, num_attention_heads=8,
+                        num_key_value_heads=2, vocab_size=256, num_hidden_layers=2)
+    gen = np.random.default_rng(3)
+    prompts = [gen.integers(0, 256, size=n).tolist() for n in (70, 33, 5)]
+    kw = dict(max_new_tokens=4, block_size=16, max_num_batched_tokens=48)
+    hip = LlamaPagedDecodeRunner(model, prompts, **kw).run()
+    ref = LlamaPagedDecodeRunner(model, prompts, prefill_attention="torch", append_backend="torch", **kw).run()
+    assert hip.prefill_batch_count > 1
+    scale = float(ref.prompt_logits.float().abs().max())
+    err = float((hip.prompt_logits.float() - ref.prompt_logits.float()).abs().max())
+    assert err <= tol * scale, (err, scale)
+    for a, b in zip(hip.decode_logits, ref.decode_logits):
+        assert float((a.float() - b.float()).abs().max()) <= 2 * tol * scale
+
+
 def test_llama_sampling_is_seeded_and_eos_stops():
     from inferkernellab_amd.llama import LlamaPagedDecodeRunner
 
