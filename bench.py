@@ -45,10 +45,12 @@ PEAK_HBM_GBPS = 8000.0
 METRIC = "paged decode attn µs/step + HBM GB/s (% peak), GQA 32/8 hd128 bf16"
 
 WORKLOADS = {
-    # name: (batch, heads, kv_heads, head_dim, dtype, ctx_lo, ctx_hi, pool, kv_scale, partition)
+    # name: (batch, heads, kv_heads, head_dim, dtype, ctx_lo, ctx_hi, pool, kv_scale, partition[, cache])
     "gqa32x8_hd128_bf16_b32_ctx4k-8k": (32, 32, 8, 128, torch.bfloat16, 4096, 8192, 20000, 1.0, None),
     "mha32_hd128_fp16_b16_ctx512": (16, 32, 32, 128, torch.float16, 512, 512, None, 1.0, None),
     "mqa32x1_hd128_bf16_b64_ctx1k-4k": (64, 32, 1, 128, torch.bfloat16, 1024, 4096, None, 0.5, None),
+    # the GQA decode shape over the FP8 (E4M3, per-row scale) cache format
+    "gqa32x8_hd128_fp8kv_b32_ctx4k-8k": (32, 32, 8, 128, torch.bfloat16, 4096, 8192, 20000, 1.0, None, "fp8"),
 }
 DEFAULT_WORKLOAD = "gqa32x8_hd128_bf16_b32_ctx4k-8k"
 
@@ -84,7 +86,8 @@ class HipEvents:
 def build_workload(name: str, device: torch.device, seed: int = 0):
     from inferkernellab_amd import PagedKVCache
 
-    batch, heads, kv_heads, head_dim, dtype, lo, hi, pool, kv_scale, _ = WORKLOADS[name]
+    batch, heads, kv_heads, head_dim, dtype, lo, hi, pool, kv_scale, _ = WORKLOADS[name][:10]
+    fp8 = len(WORKLOADS[name]) > 10 and WORKLOADS[name][10] == "fp8"
     block_size = 16
     gen = torch.Generator().manual_seed(seed)
     lengths = torch.randint(lo, hi + 1, (batch,), generator=gen).tolist()
@@ -97,10 +100,24 @@ def build_workload(name: str, device: torch.device, seed: int = 0):
         used += n
     width = max(need)
     padded = [t + [0] * (width - len(t)) for t in tables]
-    cache = PagedKVCache(pool, block_size, kv_heads, head_dim, dtype=dtype, device=device)
     dgen = torch.Generator(device=device).manual_seed(seed + 1)
-    for t in (cache.k, cache.v):
-        t.normal_(0.0, kv_scale, generator=dgen)
+    if fp8:
+        from inferkernellab_amd.cache import quantize_rows_e4m3
+
+        cache = PagedKVCache(pool, block_size, kv_heads, head_dim, dtype=torch.float8_e4m3fn, act_dtype=dtype,
+                             device=device)
+        step = 1024  # blocks quantised per chunk
+        for codes, scales in ((cache.k, cache.k_scale), (cache.v, cache.v_scale)):
+            for b0 in range(0, pool, step):
+                n = min(step, pool - b0)
+                rows = torch.randn(n, block_size, kv_heads, head_dim, generator=dgen, device=device) * kv_scale
+                c, sc = quantize_rows_e4m3(rows.to(dtype))
+                codes[0, b0 : b0 + n] = c
+                scales[0, b0 : b0 + n] = sc.transpose(1, 2)
+    else:
+        cache = PagedKVCache(pool, block_size, kv_heads, head_dim, dtype=dtype, device=device)
+        for t in (cache.k, cache.v):
+            t.normal_(0.0, kv_scale, generator=dgen)
     query = torch.randn(batch, heads, head_dim, generator=dgen, device=device, dtype=torch.float32).to(dtype)
     new_k = (torch.randn(batch, kv_heads, head_dim, generator=dgen, device=device) * kv_scale).to(dtype)
     new_v = (torch.randn(batch, kv_heads, head_dim, generator=dgen, device=device) * kv_scale).to(dtype)
@@ -116,6 +133,7 @@ def build_workload(name: str, device: torch.device, seed: int = 0):
         "new_v": new_v,
         "slots": torch.tensor(slots, dtype=torch.int32, device=device),
         "dtype": dtype,
+        "fp8": fp8,
         "heads": heads,
         "kv_heads": kv_heads,
         "head_dim": head_dim,
@@ -125,12 +143,14 @@ def build_workload(name: str, device: torch.device, seed: int = 0):
 
 
 def attention_bytes(lengths, heads: int, kv_heads: int, head_dim: int, elem_bytes: int,
-                    block_size: int, idx_bytes: int = 4) -> int:
+                    block_size: int, idx_bytes: int = 4, fp8: bool = False) -> int:
     """Algorithmic HBM bytes of one paged decode attention launch: the K+V
     rows of every context token (the reference's estimated_kv_read_bytes,
     benchmark.py:271-278, summed over ragged lengths), the q and out rows,
-    the block-table entries and the context lengths read."""
-    kv = sum(lengths) * kv_heads * head_dim * 2 * elem_bytes
+    the block-table entries and the context lengths read. With the FP8
+    cache a row is head_dim one-byte codes plus its 4-byte scale."""
+    row = head_dim + 4 if fp8 else head_dim * elem_bytes
+    kv = sum(lengths) * kv_heads * row * 2
     q_out = 2 * len(lengths) * heads * head_dim * elem_bytes
     table = sum(-(-n // block_size) for n in lengths) * idx_bytes
     return kv + q_out + table + len(lengths) * idx_bytes
@@ -139,9 +159,11 @@ def attention_bytes(lengths, heads: int, kv_heads: int, head_dim: int, elem_byte
 def step_bytes(w) -> tuple[int, int]:
     """(attention algorithmic bytes, append algorithmic bytes) of one step."""
     eb = torch.tensor([], dtype=w["dtype"]).element_size()
-    attn = attention_bytes(w["lengths"], w["heads"], w["kv_heads"], w["head_dim"], eb, w["block_size"])
+    attn = attention_bytes(w["lengths"], w["heads"], w["kv_heads"], w["head_dim"], eb, w["block_size"],
+                           fp8=w["fp8"])
     batch = len(w["lengths"])
-    append = 2 * 2 * batch * w["kv_heads"] * w["head_dim"] * eb + batch * 4  # K,V read + write, slots
+    written = w["head_dim"] + 4 if w["fp8"] else w["head_dim"] * eb  # per row: codes + scale, or the row
+    append = 2 * batch * w["kv_heads"] * (w["head_dim"] * eb + written) + batch * 4  # K,V read + write, slots
     return attn, append
 
 
@@ -168,7 +190,12 @@ def cpu_baseline(w, budget_s: float) -> dict:
         t = t.detach().cpu()
         return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
 
-    oc.k, oc.v = host(cache.k), host(cache.v)
+    if w["fp8"]:  # the oracle attends the dequantised cache
+        oc.dtype = "float32"
+        oc.k = (cache.k.float() * cache.k_scale.transpose(2, 3).unsqueeze(-1)).cpu().numpy()
+        oc.v = (cache.v.float() * cache.v_scale.transpose(2, 3).unsqueeze(-1)).cpu().numpy()
+    else:
+        oc.k, oc.v = host(cache.k), host(cache.v)
     q = po.to_f32(host(w["query"]), dtype)
     done, elapsed, kv_bytes, ctx_tokens = 0, 0.0, 0, 0
     eb = cache.k.element_size()
@@ -559,6 +586,7 @@ def main() -> int:
             "block_size": w["block_size"],
             "num_blocks": w["pool"],
             "context_tokens": sum(w["lengths"]),
+            "kv_cache": "fp8 e4m3 codes + one fp32 scale per (token, kv head)" if w["fp8"] else "same as dtype",
             "partition_size": attn.partition_size,
             "split": "balanced (equal tile runs per resident wave)" if attn.balanced_split
                      else f"fixed partitions of {attn.partition_size} tokens",

@@ -32,11 +32,14 @@
 extern "C" {
 #endif
 
-/* Element types of query / cache / key / value / output tensors. */
+/* Element types of query / cache / key / value / output tensors.
+ * IKL_FP8_E4M3 is a cache format only (cache_dtype): OCP E4M3 codes with
+ * one fp32 scale per (token, kv head) row, value = decode(code) * scale. */
 enum ikl_dtype {
   IKL_F16 = 0,
   IKL_BF16 = 1,
   IKL_F32 = 2,
+  IKL_FP8_E4M3 = 3,
 };
 
 /* Element types of index tensors (slots, block tables, context lengths). */
@@ -82,7 +85,16 @@ typedef struct ikl_append_args {
   int32_t block_size;
   int32_t num_kv_heads;
   int32_t head_dim;
-  int32_t dtype;             /* enum ikl_dtype (key, value and cache share it) */
+  int32_t dtype;             /* enum ikl_dtype of key and value (and of the cache unless cache_dtype) */
+  /* FP8 KV (no counterpart in the reference): cache_dtype IKL_FP8_E4M3
+   * quantises each appended (token, head) row — scale = amax / 448, codes =
+   * e4m3(x * 448 / amax), round to nearest even, saturating — and writes
+   * the scale to k_scale / v_scale [num_blocks, num_kv_heads, block_size]
+   * fp32 (strides in elements; the token stride is 1). 0 = same as dtype. */
+  int32_t cache_dtype;
+  void *k_scale;
+  void *v_scale;
+  int64_t scale_stride_block, scale_stride_head;
 } ikl_append_args;
 
 /* Arguments of ikl_paged_attention.
@@ -131,6 +143,14 @@ typedef struct ikl_paged_attention_args {
    * kernels of the launch: [0] before the attention kernel, [1] after it,
    * [2] after the split reduce kernel. NULL entries are skipped. */
   void *events[3];
+  /* FP8 KV cache (cache_dtype IKL_FP8_E4M3; 0 = same as dtype): the cache
+   * holds E4M3 codes with per-(token, head) fp32 scales k_scale / v_scale
+   * [num_blocks, num_kv_heads, block_size] (the layout ikl_append_kv writes).
+   * MFMA family only (dtype fp16 / bf16, head_dim in {32, 64, 96, 128}). */
+  int32_t cache_dtype;
+  const void *k_scale;
+  const void *v_scale;
+  int64_t scale_stride_block, scale_stride_head;
 } ikl_paged_attention_args;
 
 /* Arguments of ikl_rope_append_kv: rotary embedding of q and k fused with

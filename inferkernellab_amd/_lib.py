@@ -18,7 +18,7 @@ import torch  # noqa: F401  (loads the HIP runtime before the library)
 LIB_PATH = Path(__file__).resolve().parent / "libikl_paged.so"
 
 # enum ikl_dtype / ikl_index_type / ikl_status / ikl_attention_path
-IKL_F16, IKL_BF16, IKL_F32 = 0, 1, 2
+IKL_F16, IKL_BF16, IKL_F32, IKL_FP8_E4M3 = 0, 1, 2, 3
 IKL_I32, IKL_I64 = 0, 1
 IKL_OK, IKL_EINVAL, IKL_EUNSUPPORTED, IKL_ELAUNCH, IKL_EWORKSPACE = 0, -1, -2, -3, -4
 IKL_PATH_MHA_FALLBACK, IKL_PATH_SCALAR_GROUPED, IKL_PATH_MFMA_GROUPED = 0, 1, 2
@@ -68,6 +68,11 @@ class AppendArgs(ctypes.Structure):
         ("num_kv_heads", _c_i32),
         ("head_dim", _c_i32),
         ("dtype", _c_i32),
+        ("cache_dtype", _c_i32),
+        ("k_scale", _c_ptr),
+        ("v_scale", _c_ptr),
+        ("scale_stride_block", _c_i64),
+        ("scale_stride_head", _c_i64),
     ]
 
 
@@ -110,6 +115,11 @@ class PagedAttentionArgs(ctypes.Structure):
         ("workspace", _c_ptr),
         ("workspace_bytes", _c_i64),
         ("events", _c_ptr * 3),
+        ("cache_dtype", _c_i32),
+        ("k_scale", _c_ptr),
+        ("v_scale", _c_ptr),
+        ("scale_stride_block", _c_i64),
+        ("scale_stride_head", _c_i64),
     ]
 
 

@@ -10,6 +10,12 @@ and error messages follow the reference so callers see the same failures.
 The torch scatter/gather methods (``write``, ``write_slots``, ``read``) are
 the reference's ``append_backend="torch"`` path and its gather; the HIP
 append lives in :mod:`inferkernellab_amd.ops`.
+
+``dtype=torch.float8_e4m3fn`` selects the FP8 KV format (no counterpart in
+the reference): ``k`` / ``v`` hold OCP E4M3 codes and ``k_scale`` /
+``v_scale`` ``[layers, blocks, kv_heads, block_size]`` one fp32 scale per
+(token, KV head) row; ``act_dtype`` (default bfloat16) is the type of the
+rows written into it and of the queries that attend it.
 """
 
 from __future__ import annotations
@@ -17,6 +23,9 @@ from __future__ import annotations
 from dataclasses import dataclass
 
 import torch
+
+FP8_E4M3 = torch.float8_e4m3fn
+E4M3_MAX = 448.0
 
 
 @dataclass(frozen=True)
@@ -102,6 +111,7 @@ class PagedKVCache:
         num_layers: int = 1,
         dtype: torch.dtype = torch.float16,
         device: torch.device | str = "cpu",
+        act_dtype: torch.dtype | None = None,
     ):
         if min(num_layers, num_blocks, block_size, num_kv_heads, head_dim) <= 0:
             raise ValueError("cache dimensions must be positive")
@@ -111,14 +121,29 @@ class PagedKVCache:
         self.v = torch.empty_like(self.k)
         self.device = self.k.device
         self.allocator = BlockAllocator(num_blocks)
+        self.fp8 = dtype == FP8_E4M3
+        if self.fp8:
+            self.act_dtype = act_dtype or torch.bfloat16
+            if self.act_dtype not in (torch.float16, torch.bfloat16, torch.float32):
+                raise ValueError("act_dtype of an FP8 cache must be float16, bfloat16 or float32")
+            scale_shape = (num_layers, num_blocks, num_kv_heads, block_size)
+            self.k_scale = torch.ones(scale_shape, dtype=torch.float32, device=self.device)
+            self.v_scale = torch.ones_like(self.k_scale)
+        else:
+            if act_dtype is not None and act_dtype != dtype:
+                raise ValueError("act_dtype differs from dtype only for the FP8 cache")
+            self.act_dtype = dtype
+            self.k_scale = self.v_scale = None
 
     @property
     def dtype(self) -> torch.dtype:
+        """Storage type of ``k`` / ``v`` (``float8_e4m3fn`` for the FP8 cache)."""
         return self.k.dtype
 
     @property
     def numel_bytes(self) -> int:
-        return 2 * self.k.numel() * self.k.element_size()
+        scales = 2 * self.k_scale.numel() * 4 if self.fp8 else 0
+        return 2 * self.k.numel() * self.k.element_size() + scales
 
     def allocate_request(self, request_id: int, num_tokens: int) -> list[int]:
         if num_tokens <= 0:
@@ -189,6 +214,12 @@ class PagedKVCache:
         bs = self.layout.block_size
         blocks = torch.div(slots, bs, rounding_mode="floor")
         offsets = slots.remainder(bs)
+        if self.fp8:
+            for store, scales, rows in ((self.k, self.k_scale, key), (self.v, self.v_scale, value)):
+                codes, scale = quantize_rows_e4m3(rows)
+                store[layer, blocks, offsets, :, :] = codes
+                scales[layer, blocks, :, offsets] = scale
+            return
         self.k[layer, blocks, offsets, :, :] = key
         self.v[layer, blocks, offsets, :, :] = value
 
@@ -202,4 +233,25 @@ class PagedKVCache:
         bs = self.layout.block_size
         blocks = torch.div(slots, bs, rounding_mode="floor")
         offsets = slots.remainder(bs)
+        if self.fp8:  # dequantised, float32
+            k = self.k[layer, blocks, offsets].float() * self.k_scale[layer, blocks, :, offsets].unsqueeze(-1)
+            v = self.v[layer, blocks, offsets].float() * self.v_scale[layer, blocks, :, offsets].unsqueeze(-1)
+            return k, v
         return self.k[layer, blocks, offsets], self.v[layer, blocks, offsets]
+
+
+def quantize_rows_e4m3(rows: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """[..., D] rows -> (E4M3 codes [..., D], fp32 scales [...]): scale =
+    amax / 448 and codes = e4m3(x * (448 / amax)), saturated to +-448; a zero
+    row keeps scale 1. The HIP append applies the same arithmetic."""
+    x = rows.float()
+    amax = x.abs().amax(dim=-1)
+    nonzero = amax > 0
+    safe = torch.where(nonzero, amax, torch.ones_like(amax))
+    # tensor / tensor: one correctly rounded fp32 division, as the HIP kernel
+    # (a Python scalar over a tensor goes through a reciprocal: two roundings)
+    top = torch.full_like(safe, E4M3_MAX)
+    scale = torch.where(nonzero, safe / top, torch.ones_like(amax))
+    inv = torch.where(nonzero, top / safe, torch.ones_like(amax))
+    codes = (x * inv.unsqueeze(-1)).clamp(-E4M3_MAX, E4M3_MAX).to(FP8_E4M3)
+    return codes, scale

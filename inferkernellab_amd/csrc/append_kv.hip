@@ -1,5 +1,6 @@
 // KV append: scatter [T, Hkv, D] key/value rows into the paged cache
-// [num_blocks, block_size, Hkv, D] at physical slots.
+// [num_blocks, block_size, Hkv, D] at physical slots (copy), or quantise
+// them into an FP8 (E4M3) cache with per-row scales.
 //
 // Same result as cache.py:156-189 (write_slots: k[layer, slot//bs, slot%bs]
 // = key) and append.py:19-66 (_append_kv_kernel), re-laid out for gfx950:
@@ -67,7 +68,149 @@ __global__ __launch_bounds__(256) void append_kv_kernel(AppendParams p) {
   }
 }
 
+// ------------------------------------------------------------ FP8 append
+// One wave per (token, head, K or V) row: lane l converts elements
+// 4l .. 4l+3 (head_dim <= 256). The row maximum gives the scale
+// amax / 448; the codes are e4m3(x * (448 / amax)) clamped to +-448,
+// rounded to nearest even by v_cvt_pk_fp8_f32 (OCP E4M3 on gfx950). A zero
+// row keeps scale 1.
+struct Fp8AppendParams {
+  const char *src[2];         // key, value rows
+  int64_t src_st[2], src_sh[2];  // bytes
+  const void *slots;
+  char *dst[2];               // fp8 caches
+  int64_t dst_sb[2], dst_st[2], dst_sh[2];  // bytes (= elements)
+  float *scale[2];
+  int64_t scale_sb, scale_sh;  // elements
+  int64_t num_slots;
+  int32_t block_size;
+  int32_t head_dim;
+};
+
+template <typename Tag>
+__device__ inline void load4(const char *p, float *x);
+template <>
+__device__ inline void load4<bf16_tag>(const char *p, float *x) {
+  const uint2 w = *reinterpret_cast<const uint2 *>(p);
+  x[0] = elem<bf16_tag>::lo(w.x);
+  x[1] = elem<bf16_tag>::hi(w.x);
+  x[2] = elem<bf16_tag>::lo(w.y);
+  x[3] = elem<bf16_tag>::hi(w.y);
+}
+template <>
+__device__ inline void load4<f16_tag>(const char *p, float *x) {
+  const uint2 w = *reinterpret_cast<const uint2 *>(p);
+  x[0] = elem<f16_tag>::lo(w.x);
+  x[1] = elem<f16_tag>::hi(w.x);
+  x[2] = elem<f16_tag>::lo(w.y);
+  x[3] = elem<f16_tag>::hi(w.y);
+}
+template <>
+__device__ inline void load4<f32_tag>(const char *p, float *x) {
+  const float4 w = *reinterpret_cast<const float4 *>(p);
+  x[0] = w.x;
+  x[1] = w.y;
+  x[2] = w.z;
+  x[3] = w.w;
+}
+
+__device__ inline float wave_max(float v) {
+  v = fmaxf(v, dpp_mov<DPP_QUAD_XOR1>(v));
+  v = fmaxf(v, dpp_mov<DPP_QUAD_XOR2>(v));
+  v = fmaxf(v, dpp_mov<DPP_ROW_HALF_MIRROR>(v));
+  v = fmaxf(v, dpp_mov<DPP_ROW_MIRROR>(v));
+  return max_xor32(max_xor16(v));
+}
+
+template <typename Tag, typename IdxT>
+__global__ __launch_bounds__(64) void append_kv_fp8_kernel(Fp8AppendParams p) {
+  constexpr int EB = elem<Tag>::bytes;
+  const int lane = threadIdx.x;
+  const int which = blockIdx.x & 1;  // 0: key, 1: value
+  const int h = (int)(blockIdx.x >> 1);
+  const int64_t t = blockIdx.y;
+  const int64_t slot = (int64_t)reinterpret_cast<const IdxT *>(p.slots)[t];
+  if (slot < 0 || slot >= p.num_slots) return;
+  const int64_t blk = slot / p.block_size;
+  const int64_t off = slot - blk * p.block_size;
+  const bool on = 4 * lane < p.head_dim;
+  float x[4] = {0.f, 0.f, 0.f, 0.f};
+  if (on) load4<Tag>(p.src[which] + t * p.src_st[which] + h * p.src_sh[which] + 4 * lane * EB, x);
+  const float amax = wave_max(fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))));
+  const float scale = amax > 0.f ? amax / 448.0f : 1.0f;
+  const float inv = amax > 0.f ? 448.0f / amax : 1.0f;
+  float y[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) y[i] = fminf(fmaxf(x[i] * inv, -448.0f), 448.0f);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w, true);
+  if (on) *reinterpret_cast<int *>(p.dst[which] + blk * p.dst_sb[which] + off * p.dst_st[which] + h * p.dst_sh[which] + 4 * lane) = w;
+  if (lane == 0) p.scale[which][blk * p.scale_sb + h * p.scale_sh + off] = scale;
+}
+
 bool aligned(const void *ptr, int64_t n) { return ((uintptr_t)ptr % (uintptr_t)n) == 0; }
+
+int append_fp8(const ikl_append_args *a, hipStream_t s) {
+  int eb;
+  switch (a->dtype) {
+    case IKL_F16:
+    case IKL_BF16: eb = 2; break;
+    case IKL_F32: eb = 4; break;
+    default: return fail(IKL_EINVAL, "append: unsupported dtype");
+  }
+  if (a->head_dim % 4 != 0 || a->head_dim > 256)
+    return fail(IKL_EUNSUPPORTED, "append: the FP8 cache needs head_dim a multiple of 4, at most 256");
+  if (!a->k_scale || !a->v_scale) return fail(IKL_EINVAL, "append: the FP8 cache needs k_scale and v_scale");
+  Fp8AppendParams p;
+  p.src[0] = (const char *)a->key;
+  p.src[1] = (const char *)a->value;
+  p.src_st[0] = a->key_stride_t * eb;
+  p.src_sh[0] = a->key_stride_h * eb;
+  p.src_st[1] = a->value_stride_t * eb;
+  p.src_sh[1] = a->value_stride_h * eb;
+  p.slots = a->slots;
+  p.dst[0] = (char *)a->k_cache;
+  p.dst[1] = (char *)a->v_cache;
+  p.dst_sb[0] = a->k_stride_block;
+  p.dst_st[0] = a->k_stride_token;
+  p.dst_sh[0] = a->k_stride_head;
+  p.dst_sb[1] = a->v_stride_block;
+  p.dst_st[1] = a->v_stride_token;
+  p.dst_sh[1] = a->v_stride_head;
+  p.scale[0] = (float *)a->k_scale;
+  p.scale[1] = (float *)a->v_scale;
+  p.scale_sb = a->scale_stride_block;
+  p.scale_sh = a->scale_stride_head;
+  p.num_slots = a->num_blocks * (int64_t)a->block_size;
+  p.block_size = a->block_size;
+  p.head_dim = a->head_dim;
+  // every row the kernel touches is read 4 elements and written 4 codes at a time
+  const int64_t in_steps[] = {p.src_st[0], p.src_sh[0], p.src_st[1], p.src_sh[1]};
+  for (int64_t st : in_steps)
+    if (st % (4 * eb) != 0) return fail(IKL_EINVAL, "append: key/value rows must be aligned to 4 elements");
+  const int64_t out_steps[] = {p.dst_sb[0], p.dst_st[0], p.dst_sh[0], p.dst_sb[1], p.dst_st[1], p.dst_sh[1]};
+  for (int64_t st : out_steps)
+    if (st % 4 != 0) return fail(IKL_EINVAL, "append: FP8 cache rows must be 4-byte aligned");
+  if (!aligned(a->key, 4 * eb) || !aligned(a->value, 4 * eb) || !aligned(a->k_cache, 4) ||
+      !aligned(a->v_cache, 4) || !aligned(a->k_scale, 4) || !aligned(a->v_scale, 4))
+    return fail(IKL_EINVAL, "append: misaligned tensor pointer");
+  if ((int64_t)a->num_kv_heads * 2 > 0x7fffffffLL) return fail(IKL_EINVAL, "append: too many heads");
+  const dim3 grid((unsigned)(2 * a->num_kv_heads), (unsigned)a->num_tokens);
+#define IKL_FP8_LAUNCH(TAG, IDX) append_kv_fp8_kernel<TAG, IDX><<<grid, 64, 0, s>>>(p)
+  const bool i32 = a->slot_type == IKL_I32;
+  if (a->dtype == IKL_BF16) {
+    if (i32) IKL_FP8_LAUNCH(bf16_tag, int32_t);
+    else IKL_FP8_LAUNCH(bf16_tag, int64_t);
+  } else if (a->dtype == IKL_F16) {
+    if (i32) IKL_FP8_LAUNCH(f16_tag, int32_t);
+    else IKL_FP8_LAUNCH(f16_tag, int64_t);
+  } else {
+    if (i32) IKL_FP8_LAUNCH(f32_tag, int32_t);
+    else IKL_FP8_LAUNCH(f32_tag, int64_t);
+  }
+#undef IKL_FP8_LAUNCH
+  return check_launch("append_kv_fp8_kernel");
+}
 
 }  // namespace
 }  // namespace ikl
@@ -85,6 +228,9 @@ extern "C" int ikl_append_kv(const ikl_append_args *a, void *stream) {
     return fail(IKL_EINVAL, "append: null tensor pointer");
   if (a->slot_type != IKL_I32 && a->slot_type != IKL_I64)
     return fail(IKL_EINVAL, "append: slots must use int32 or int64");
+  if (a->cache_dtype == IKL_FP8_E4M3) return append_fp8(a, (hipStream_t)stream);
+  if (a->cache_dtype != 0 && a->cache_dtype != a->dtype)
+    return fail(IKL_EINVAL, "append: cache_dtype must be 0, the key dtype or IKL_FP8_E4M3");
   int eb;
   switch (a->dtype) {
     case IKL_F16:

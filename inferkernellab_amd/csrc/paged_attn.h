@@ -53,6 +53,12 @@ struct AttnParams {
   int32_t units;           // kv heads x query groups per request
   int64_t batch;
   int64_t cap_tokens;      // table_width * block_size: positions a table can map
+  // FP8 KV cache (MFMA family): E4M3 codes with one fp32 scale per (token,
+  // head) row in k_scale / v_scale [blocks, kv heads, block_size].
+  int32_t kv_fp8;
+  const float *k_scale;
+  const float *v_scale;
+  int64_t s_sb, s_sh;      // elements
 };
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -168,6 +174,6 @@ MfmaShape mfma_launch_shape(bool balanced, int group_size);
 
 // One-wave workgroups of the balanced-split MFMA kernel (for units of
 // `group_size` heads) resident at once on the current device.
-int mfma_streamk_capacity(int dtype, int head_dim, int group_size);
+int mfma_streamk_capacity(int dtype, int head_dim, int group_size, bool kv_fp8);
 
 }  // namespace ikl

@@ -416,6 +416,7 @@ struct Plan {
   int64_t units = 0;  // kv heads x query groups per request
   int64_t ws_o_bytes = 0;
   int64_t ws_bytes = 0;
+  bool kv_fp8 = false;  // E4M3 cache with per-row scales (MFMA family only)
 };
 
 int elem_bytes(int dtype) {
@@ -472,7 +473,15 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
   if (a->query_group_size < 0) return fail(IKL_EINVAL, "query_group_size must be non-negative");
   pl.heads_per_kv = a->num_heads / a->num_kv_heads;
   const int requested_gs = a->query_group_size;
-  if (a->path == -1) {
+  if (a->cache_dtype != 0 && a->cache_dtype != a->dtype && a->cache_dtype != IKL_FP8_E4M3)
+    return fail(IKL_EINVAL, "attention: cache_dtype must be 0, the query dtype or IKL_FP8_E4M3");
+  pl.kv_fp8 = a->cache_dtype == IKL_FP8_E4M3;
+  if (pl.kv_fp8) {
+    // the FP8 cache is read by the MFMA family only (any heads per KV head)
+    if (a->path != -1 && a->path != IKL_PATH_MFMA_GROUPED)
+      return fail(IKL_EUNSUPPORTED, "attention: the FP8 cache is read by the MFMA family only");
+    pl.path = IKL_PATH_MFMA_GROUPED;
+  } else if (a->path == -1) {
     pl.path = select_path(a->dtype, a->head_dim, a->block_size, pl.heads_per_kv, requested_gs);
   } else if (a->path == IKL_PATH_MHA_FALLBACK || a->path == IKL_PATH_SCALAR_GROUPED) {
     pl.path = pl.heads_per_kv == 1 ? IKL_PATH_MHA_FALLBACK : a->path;
@@ -486,8 +495,10 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
   const int cap_gs = pl.path == IKL_PATH_MFMA_GROUPED ? MFMA_MAX_GROUP : SCALAR_MAX_GROUP;
   if (gs > cap_gs) gs = cap_gs;
   if (pl.path == IKL_PATH_MFMA_GROUPED && !mfma_supported(a->dtype, a->head_dim, a->block_size, gs))
-    return fail(IKL_EUNSUPPORTED,
-                "MFMA path needs fp16/bf16, head_dim 32/64/96/128 and a block size multiple of 16");
+    return fail(IKL_EUNSUPPORTED, pl.kv_fp8 ? "the FP8 cache needs fp16/bf16 queries, head_dim 32/64/96/128 and "
+                                              "a block size multiple of 16"
+                                            : "MFMA path needs fp16/bf16, head_dim 32/64/96/128 and a block size "
+                                              "multiple of 16");
   pl.group_size = gs;
   pl.gmax = next_pow2(gs);
   pl.groups_per_kv = (pl.heads_per_kv + gs - 1) / gs;
@@ -504,7 +515,7 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
   // (T + 1) * W to fit in 63 bits.
   if (a->partition_size == 0 && pl.path == IKL_PATH_MFMA_GROUPED && cap < (int64_t(1) << 29)) {
     const int64_t t_max = units * ((maxctx + 15) / 16);
-    const int64_t w = std::min<int64_t>(mfma_streamk_capacity(a->dtype, a->head_dim, pl.group_size), std::max<int64_t>(t_max, 1));
+    const int64_t w = std::min<int64_t>(mfma_streamk_capacity(a->dtype, a->head_dim, pl.group_size, pl.kv_fp8), std::max<int64_t>(t_max, 1));
     if ((double)(t_max + 1) * (double)w < 4.0e18) {
       pl.sk_waves = (int)w;
       pl.split = true;
@@ -681,13 +692,17 @@ extern "C" int ikl_paged_attention(const ikl_paged_attention_args *a, void *stre
   if (!a->query || !a->k_cache || !a->v_cache || !a->block_tables || !a->context_lens || !a->out)
     return fail(IKL_EINVAL, "attention: null tensor pointer");
   const int vec = 16 / pl.eb;
+  const int cvec = pl.kv_fp8 ? 16 : vec;  // cache elements per 16 bytes
   // 16-byte vector access needs every row start 16-byte aligned.
   if (!aligned16(a->query) || !aligned16(a->k_cache) || !aligned16(a->v_cache) || !aligned16(a->out) ||
-      a->q_stride_b % vec || a->q_stride_h % vec || a->k_stride_block % vec ||
-      a->k_stride_token % vec || a->k_stride_head % vec || a->v_stride_block % vec ||
-      a->v_stride_token % vec || a->v_stride_head % vec || a->out_stride_b % vec ||
+      a->q_stride_b % vec || a->q_stride_h % vec || a->k_stride_block % cvec ||
+      a->k_stride_token % cvec || a->k_stride_head % cvec || a->v_stride_block % cvec ||
+      a->v_stride_token % cvec || a->v_stride_head % cvec || a->out_stride_b % vec ||
       a->out_stride_h % vec)
     return fail(IKL_EINVAL, "attention: query/cache/out rows must be 16-byte aligned");
+  if (pl.kv_fp8 && (!a->k_scale || !a->v_scale || !aligned16(a->k_scale) || !aligned16(a->v_scale) ||
+                    a->scale_stride_block % 4 || a->scale_stride_head % 4))
+    return fail(IKL_EINVAL, "attention: the FP8 cache needs 16-byte aligned k_scale / v_scale rows");
   if (pl.split && (!a->workspace || a->workspace_bytes < pl.ws_bytes || !aligned16(a->workspace)))
     return fail(IKL_EWORKSPACE, "attention: workspace missing or smaller than " +
                                     std::to_string(pl.ws_bytes) + " bytes");
@@ -732,6 +747,11 @@ extern "C" int ikl_paged_attention(const ikl_paged_attention_args *a, void *stre
   p.units = (int32_t)pl.units;
   p.batch = a->batch;
   p.cap_tokens = a->table_width * (int64_t)a->block_size;
+  p.kv_fp8 = pl.kv_fp8 ? 1 : 0;
+  p.k_scale = (const float *)a->k_scale;
+  p.v_scale = (const float *)a->v_scale;
+  p.s_sb = a->scale_stride_block;
+  p.s_sh = a->scale_stride_head;
 
   dim3 grid((unsigned)pl.num_parts, (unsigned)(a->num_kv_heads * pl.groups_per_kv), (unsigned)a->batch);
   hipStream_t s = (hipStream_t)stream;

@@ -59,30 +59,66 @@ constexpr bool split_p() {
   return IKL_MFMA_SPLIT_P != 0 && mfma_ops<Tag>::NARROW_P;
 }
 
+// Two E4M3 codes -> two bf16 / fp16 values (exact: every E4M3 value is a
+// bf16 and an fp16 value), as one packed dword. `hi` selects the upper
+// code pair of `w`.
+template <typename Tag>
+__device__ inline uint32_t fp8x2_to(uint32_t w, bool hi);
+template <>
+__device__ inline uint32_t fp8x2_to<bf16_tag>(uint32_t w, bool hi) {
+  return __builtin_bit_cast(uint32_t, hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true)
+                                        : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+}
+template <>
+__device__ inline uint32_t fp8x2_to<f16_tag>(uint32_t w, bool hi) {
+  return __builtin_bit_cast(uint32_t, hi ? __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true)
+                                        : __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+}
+// Eight codes (two dwords) -> one 16-byte MFMA operand of 8 elements.
+template <typename Tag>
+__device__ inline v4u32 fp8x8_to(uint32_t lo, uint32_t hi) {
+  return v4u32{fp8x2_to<Tag>(lo, false), fp8x2_to<Tag>(lo, true), fp8x2_to<Tag>(hi, false),
+               fp8x2_to<Tag>(hi, true)};
+}
+
 // Per-wave state of the tile loop: lane constants, the Q^T operands and the
 // running softmax states (acc, m, lsum) of one (request, unit) run. A unit
 // has up to NG * 16 query heads: NG 16-head MFMA groups share every K/V tile
 // the wave loads (NG = 2 serves 32-head groups such as MQA-32 without
 // reading K/V twice).
-template <typename Tag, int D, int NG>
+//
+// KV8: the cache holds E4M3 codes with one fp32 scale per (token, head)
+// row. K codes are widened in registers (the k order inside the QK^T
+// product is free as long as Q uses the same one, so lane group g takes
+// the contiguous elements [8 KSTEPS g, 8 KSTEPS (g + 1))), each score is
+// multiplied by its token's K scale, the probabilities that enter the PV
+// product by the token's V scale (the softmax sum keeps the unscaled
+// ones), and V codes are widened on their way into the same LDS tile the
+// 16-bit path stages.
+template <typename Tag, int D, int NG, bool KV8>
 struct WaveTiles {
   static_assert(D % 32 == 0 && D <= 128, "MFMA path needs head_dim = 32k <= 128");
   static_assert(NG == 1 || NG == 2, "one or two 16-head groups per wave");
   static constexpr int EB = 2;
+  static constexpr int CEB = KV8 ? 1 : 2;                   // bytes per cache element
   static constexpr int NH = 16 * NG;                        // query heads per wave
   static constexpr int KSTEPS = D / 32;                     // QK^T k-steps
   static constexpr int MTILES = D / 16;                     // PV output tiles of 16 dims
-  static constexpr int PIECES = D * EB / 16;                // 16-byte pieces per row
-  static constexpr int ROWB = D * EB;                       // bytes per K/V row
-  static constexpr int VLOADS = (TILE * PIECES + 63) / 64;  // 16-byte V loads per lane per tile
+  static constexpr int PIECES = D * EB / 16;                // 16-byte pieces per staged (16-bit) row
+  static constexpr int ROWB = D * EB;                       // bytes per staged row
+  static constexpr int CPIECES = D * CEB / 16;              // 16-byte pieces per cache row
+  static constexpr int VLOADS = (TILE * CPIECES + 63) / 64; // 16-byte V loads per lane per tile
   static constexpr int VT_BYTES = TILE * ROWB;              // one staged V tile
   static constexpr int SROW = D + 4;                        // staged fp32 row (padded vs bank conflicts)
   static constexpr int ST_BYTES = NH * SROW * 4;            // one staged [NH heads x D] block
   using ops = mfma_ops<Tag>;
+  typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+  typedef const __attribute__((address_space(1))) u32x2v *global_u32x2_ptr;
 
   struct Tile {
-    v4u32 k[KSTEPS];
+    v4u32 k[KSTEPS];       // 16-bit: one operand per k-step; KV8: raw codes, 8 bytes per k-step
     v4u32 v[VLOADS];
+    f32x4_t ks, vs;        // KV8: scales of tokens 4 grp .. +3
     int n_valid;  // tokens of the tile inside the run with a valid block (0..16)
   };
 
@@ -93,17 +129,23 @@ struct WaveTiles {
   f32x4_t acc[NG][MTILES];
   float m[NG], lsum[NG];
 
+  // element offset of k-step s inside a row for this lane
+  __device__ __forceinline__ int k_elem(int s) const { return KV8 ? 8 * KSTEPS * grp + 8 * s : 32 * s + 8 * grp; }
+
   __device__ __forceinline__ explicit WaveTiles(const AttnParams &p) {
     lane = threadIdx.x & 63;
     hl = lane & 15;   // MFMA row/column index inside a 16-lane group
     grp = lane >> 4;  // 16-lane group
-    k_lane = (hl * (int)p.k_st + 8 * grp) * EB;  // token hl, dims 8g.. of each k-step
+    k_lane = (hl * (int)p.k_st + k_elem(0)) * CEB;  // token hl, first element of k-step 0
 #pragma unroll
     for (int u = 0; u < VLOADS; ++u) {
-      const int pi = u * 64 + lane;  // V piece: row pi / PIECES, piece pi % PIECES
-      const int row = pi / PIECES < TILE ? pi / PIECES : TILE - 1, c = pi % PIECES;
-      v_lds[u] = row * ROWB + ((c + row) % PIECES) * 16;
-      v_lane[u] = row * (int)p.v_st * EB + c * 16;
+      // V cache piece: row pi / CPIECES, piece pi % CPIECES; for KV8 it widens
+      // into staged pieces 2c, 2c + 1
+      const int pi = u * 64 + lane;
+      const int row = pi / CPIECES < TILE ? pi / CPIECES : TILE - 1, c = pi % CPIECES;
+      const int sc = KV8 ? 2 * c : c;
+      v_lds[u] = row * ROWB + ((sc + row) % PIECES) * 16;
+      v_lane[u] = row * (int)p.v_st * CEB + c * 16;
     }
 #pragma unroll
     for (int mt = 0; mt < MTILES; ++mt) {  // V^T reads: token 4g + (l%16)/4, dims 16mt + 4((l%16)%4)
@@ -113,7 +155,7 @@ struct WaveTiles {
     }
   }
 
-  // Q^T operands: in group g, lane l holds q[hq0 + 16g + l%16][32s + 8(l/16) .. +7]
+  // Q^T operands: in group g, lane l holds q[hq0 + 16g + l%16][k_elem(s) .. +7]
   // (zero for heads >= nh).
   __device__ __forceinline__ void load_q(const AttnParams &p, int64_t b, int64_t hq0, int nh) {
 #pragma unroll
@@ -122,7 +164,7 @@ struct WaveTiles {
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s) {
         qb[g][s] = zero4();
-        if (h < nh) qb[g][s] = load16v_global(p.q + (b * p.q_sb + (hq0 + h) * p.q_sh + 32 * s + 8 * grp) * EB);
+        if (h < nh) qb[g][s] = load16v_global(p.q + (b * p.q_sb + (hq0 + h) * p.q_sh + k_elem(s)) * EB);
       }
     }
   }
@@ -140,8 +182,8 @@ struct WaveTiles {
       lsum[g] = 0.f;
     }
     const int n_tiles = t1 > t0 ? (int)((t1 - t0 + TILE - 1) / TILE) : 0;
-    const char *kbase = p.kc + (int64_t)kvh * p.k_sh * EB;
-    const char *vbase = p.vc + (int64_t)kvh * p.v_sh * EB;
+    const char *kbase = p.kc + (int64_t)kvh * p.k_sh * CEB;
+    const char *vbase = p.vc + (int64_t)kvh * p.v_sh * CEB;
     const char *zero_row = reinterpret_cast<const char *>(g_zero_row);
     const int bs = p.block_size;
     int64_t win_base = p.bs_shift >= 0 ? (t0 >> p.bs_shift) : t0 / bs;
@@ -160,16 +202,40 @@ struct WaveTiles {
       const int phys = __builtin_amdgcn_readlane(win, (int)(lb - win_base));
       const int64_t left = t1 - base;
       T.n_valid = phys < 0 || left <= 0 ? 0 : (left >= TILE ? TILE : (int)left);
-      const int64_t kro = ((int64_t)phys * p.k_sb + off * p.k_st) * EB;
-      const int64_t vro = ((int64_t)phys * p.v_sb + off * p.v_st) * EB;
+      const int64_t kro = ((int64_t)phys * p.k_sb + off * p.k_st) * CEB;
+      const int64_t vro = ((int64_t)phys * p.v_sb + off * p.v_st) * CEB;
       const bool k_ok = hl < T.n_valid;
       const char *kr = k_ok ? kbase + kro + k_lane : zero_row;
-      const int kstep = k_ok ? 64 : 0;
+      if constexpr (KV8) {
+        // KSTEPS contiguous 8-byte chunks at 8 KSTEPS grp: paired into
+        // 16-byte loads when KSTEPS is even (then 16-byte aligned), else
+        // 8-byte loads. T.k[s & ~1] holds k-step s (dwords xy for even s).
+        if constexpr (KSTEPS % 2 == 0) {
+          const int kstep = k_ok ? 16 : 0;
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) T.k[s] = load16v_stream(kr + s * kstep);
+          for (int s = 0; s < KSTEPS; s += 2) T.k[s] = load16v_stream(kr + (s / 2) * kstep);
+        } else {
+          const int kstep = k_ok ? 8 : 0;
+#pragma unroll
+          for (int s = 0; s < KSTEPS; ++s) {
+            const u32x2v w = __builtin_nontemporal_load((global_u32x2_ptr)(kr + s * kstep));
+            if (s % 2 == 0) T.k[s] = v4u32{w.x, w.y, 0u, 0u};
+            else T.k[s - 1] = v4u32{T.k[s - 1].x, T.k[s - 1].y, w.x, w.y};
+          }
+        }
+        // scales of tokens 4 grp .. +3 (16 bytes; a masked tile reads the zero row)
+        const bool s_ok = T.n_valid > 0;
+        const int64_t so = ((int64_t)phys * p.s_sb + (int64_t)kvh * p.s_sh + off + 4 * grp) * 4;
+        T.ks = __builtin_bit_cast(f32x4_t, load16v_stream(s_ok ? (const char *)p.k_scale + so : zero_row));
+        T.vs = __builtin_bit_cast(f32x4_t, load16v_stream(s_ok ? (const char *)p.v_scale + so : zero_row));
+      } else {
+        const int kstep = k_ok ? 64 : 0;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) T.k[s] = load16v_stream(kr + s * kstep);
+      }
 #pragma unroll
       for (int u = 0; u < VLOADS; ++u) {
-        const int row = (u * 64 + lane) / PIECES;
+        const int row = (u * 64 + lane) / CPIECES;
         const bool v_ok = row < T.n_valid;
         T.v[u] = load16v_stream(v_ok ? vbase + vro + v_lane[u] : zero_row);
       }
@@ -179,16 +245,44 @@ struct WaveTiles {
       // stage V row-major in LDS (rows past the tile are never read)
 #pragma unroll
       for (int u = 0; u < VLOADS; ++u) {
-        if (TILE * PIECES % 64 == 0 || u * 64 + lane < TILE * PIECES)
-          *reinterpret_cast<v4u32 *>(vtile + v_lds[u]) = T.v[u];
+        if (TILE * CPIECES % 64 == 0 || u * 64 + lane < TILE * CPIECES) {
+          if constexpr (KV8) {
+            const int row = (u * 64 + lane) / CPIECES;
+            const int c2 = (((v_lds[u] - row * ROWB) / 16) + 1) % PIECES;  // rotated slot of piece 2c + 1
+            *reinterpret_cast<v4u32 *>(vtile + v_lds[u]) = fp8x8_to<Tag>(T.v[u].x, T.v[u].y);
+            *reinterpret_cast<v4u32 *>(vtile + row * ROWB + c2 * 16) = fp8x8_to<Tag>(T.v[u].z, T.v[u].w);
+          } else {
+            *reinterpret_cast<v4u32 *>(vtile + v_lds[u]) = T.v[u];
+          }
+        }
       }
       // S^T of each group for tokens 4g' + i and head hl
+      v4u32 ka[KSTEPS];
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        if constexpr (KV8) {
+          const v4u32 w = T.k[s & ~1];
+          ka[s] = (s & 1) == 0 ? fp8x8_to<Tag>(w.x, w.y) : fp8x8_to<Tag>(w.z, w.w);
+        } else {
+          ka[s] = T.k[s];
+        }
+      }
       f32x4_t sa[NG];
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         sa[g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) sa[g] = ops::mma_k32(T.k[s], qb[g][s], sa[g]);
+        for (int s = 0; s < KSTEPS; ++s) sa[g] = ops::mma_k32(ka[s], qb[g][s], sa[g]);
+      }
+      f32x4_t kscale = f32x4_t{p.scale_log2, p.scale_log2, p.scale_log2, p.scale_log2};
+      f32x4_t vscale = f32x4_t{1.f, 1.f, 1.f, 1.f};
+      if constexpr (KV8) {
+        kscale = T.ks * p.scale_log2;
+        vscale = T.vs;
+        if (T.n_valid < TILE) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) vscale[i] = 4 * grp + i < T.n_valid ? vscale[i] : 0.f;
+        }
       }
       u32x2_t pb[NG], pl[NG];
 #pragma unroll
@@ -196,7 +290,7 @@ struct WaveTiles {
         float sc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          sc[i] = sa[g][i] * p.scale_log2;
+          sc[i] = sa[g][i] * kscale[i];
           if (T.n_valid < TILE) sc[i] = 4 * grp + i < T.n_valid ? sc[i] : -INFINITY;
         }
         float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
@@ -214,6 +308,7 @@ struct WaveTiles {
         for (int i = 0; i < 4; ++i) {
           pr[i] = fast_exp2(sc[i] - m[g]);
           lsum[g] += pr[i];
+          if constexpr (KV8) pr[i] *= vscale[i];  // the PV product takes p * v_scale
         }
         pb[g] = u32x2_t{ops::pack(pr[0], pr[1]), ops::pack(pr[2], pr[3])};
         // A bf16 P keeps 8 significant bits; with SPLIT_P its rounding
@@ -315,10 +410,10 @@ __device__ __forceinline__ void store_rows_out(const AttnParams &p, int64_t b, i
   }
 }
 
-template <typename Tag, int D, int NG, int WAVES>
+template <typename Tag, int D, int NG, int WAVES, bool KV8>
 __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_kernel(const AttnParams p) {
   static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4, "1, 2 or 4 waves per workgroup");
-  using WT = WaveTiles<Tag, D, NG>;
+  using WT = WaveTiles<Tag, D, NG, KV8>;
   constexpr int NH = WT::NH;
   // LDS: each wave's V tile during the loop; at the end each wave's staged
   // [NH heads x D] block, which the workgroup sums. The uses never overlap.
@@ -413,9 +508,9 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
 // units x tiles of all requests, W = min(sk_waves, T)) piece by piece — a
 // piece is the part of one (request, unit) inside the run — and writes each
 // piece's normalised output and log2-sum-exp to partial slot unit + w.
-template <typename Tag, int D, int NG>
+template <typename Tag, int D, int NG, bool KV8>
 __global__ __launch_bounds__(64) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_streamk_kernel(const AttnParams p) {
-  using WT = WaveTiles<Tag, D, NG>;
+  using WT = WaveTiles<Tag, D, NG, KV8>;
   constexpr int NH = WT::NH;
   constexpr int SLOT = WT::ST_BYTES > WT::VT_BYTES ? WT::ST_BYTES : WT::VT_BYTES;
   __shared__ __attribute__((aligned(16))) char lds[SLOT];
@@ -505,34 +600,40 @@ constexpr int wg_waves() {
   return NG == 1 ? IKL_MFMA_WG_WAVES : 2;
 }
 
-template <typename Tag, int D, int NG>
+template <typename Tag, int D, int NG, bool KV8>
 void launch_shape(const AttnParams &p, dim3 grid, hipStream_t s) {
   if (p.sk_waves > 0) {
-    paged_decode_mfma_streamk_kernel<Tag, D, NG><<<dim3((unsigned)p.sk_waves), 64, 0, s>>>(p);
+    paged_decode_mfma_streamk_kernel<Tag, D, NG, KV8><<<dim3((unsigned)p.sk_waves), 64, 0, s>>>(p);
     return;
   }
 #if IKL_MFMA_HEAD_MAJOR
   grid = dim3(grid.y, grid.x, grid.z);
 #endif
   constexpr int WAVES = wg_waves<NG>();
-  paged_decode_mfma_kernel<Tag, D, NG, WAVES><<<grid, dim3(64 * WAVES), 0, s>>>(p);
+  paged_decode_mfma_kernel<Tag, D, NG, WAVES, KV8><<<grid, dim3(64 * WAVES), 0, s>>>(p);
+}
+
+template <typename Tag, int NG, bool KV8>
+void launch_dim(int d, const AttnParams &p, dim3 grid, hipStream_t s) {
+  switch (d) {
+    case 32: launch_shape<Tag, 32, NG, KV8>(p, grid, s); break;
+    case 64: launch_shape<Tag, 64, NG, KV8>(p, grid, s); break;
+    case 96: launch_shape<Tag, 96, NG, KV8>(p, grid, s); break;
+    default: launch_shape<Tag, 128, NG, KV8>(p, grid, s); break;
+  }
 }
 
 template <typename Tag, int NG>
-void launch_dim(int d, const AttnParams &p, dim3 grid, hipStream_t s) {
-  switch (d) {
-    case 32: launch_shape<Tag, 32, NG>(p, grid, s); break;
-    case 64: launch_shape<Tag, 64, NG>(p, grid, s); break;
-    case 96: launch_shape<Tag, 96, NG>(p, grid, s); break;
-    default: launch_shape<Tag, 128, NG>(p, grid, s); break;
-  }
+void launch_kv(int d, const AttnParams &p, dim3 grid, hipStream_t s) {
+  if (p.kv_fp8) launch_dim<Tag, NG, true>(d, p, grid, s);
+  else launch_dim<Tag, NG, false>(d, p, grid, s);
 }
 
 // Resident one-wave workgroups of the balanced-split kernel on the current
 // device (CUs x workgroups per CU), cached per device; 256 CUs x the
 // kernel's waves per CU (8 for 16-head units, 4 for 32-head) when no device
 // answers (planning on a host without a GPU).
-template <typename Tag, int D, int NG>
+template <typename Tag, int D, int NG, bool KV8>
 int streamk_capacity_for() {
   constexpr int MAX_DEV = 64;
   constexpr int FALLBACK = 256 * (NG == 1 ? 8 : 4);
@@ -545,8 +646,8 @@ int streamk_capacity_for() {
   if (cache[dev] > 0) return cache[dev];
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_mfma_streamk_kernel<Tag, D, NG>, 64, 0) !=
-          hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_mfma_streamk_kernel<Tag, D, NG, KV8>, 64,
+                                                   0) != hipSuccess ||
       cus <= 0 || per_cu <= 0) {
     (void)hipGetLastError();
     return FALLBACK;
@@ -555,14 +656,19 @@ int streamk_capacity_for() {
   return cache[dev];
 }
 
-template <typename Tag, int NG>
+template <typename Tag, int NG, bool KV8>
 int capacity_dim(int d) {
   switch (d) {
-    case 32: return streamk_capacity_for<Tag, 32, NG>();
-    case 64: return streamk_capacity_for<Tag, 64, NG>();
-    case 96: return streamk_capacity_for<Tag, 96, NG>();
-    default: return streamk_capacity_for<Tag, 128, NG>();
+    case 32: return streamk_capacity_for<Tag, 32, NG, KV8>();
+    case 64: return streamk_capacity_for<Tag, 64, NG, KV8>();
+    case 96: return streamk_capacity_for<Tag, 96, NG, KV8>();
+    default: return streamk_capacity_for<Tag, 128, NG, KV8>();
   }
+}
+
+template <typename Tag, int NG>
+int capacity_kv(int d, bool kv8) {
+  return kv8 ? capacity_dim<Tag, NG, true>(d) : capacity_dim<Tag, NG, false>(d);
 }
 
 }  // namespace
@@ -576,11 +682,11 @@ bool mfma_supported(int dtype, int head_dim, int block_size, int group_size) {
 hipError_t launch_mfma_attention(int dtype, int head_dim, const AttnParams &p, dim3 grid, hipStream_t s) {
   const bool two = p.group_size > 16;
   if (dtype == IKL_BF16) {
-    if (two) launch_dim<bf16_tag, 2>(head_dim, p, grid, s);
-    else launch_dim<bf16_tag, 1>(head_dim, p, grid, s);
+    if (two) launch_kv<bf16_tag, 2>(head_dim, p, grid, s);
+    else launch_kv<bf16_tag, 1>(head_dim, p, grid, s);
   } else {
-    if (two) launch_dim<f16_tag, 2>(head_dim, p, grid, s);
-    else launch_dim<f16_tag, 1>(head_dim, p, grid, s);
+    if (two) launch_kv<f16_tag, 2>(head_dim, p, grid, s);
+    else launch_kv<f16_tag, 1>(head_dim, p, grid, s);
   }
   return hipGetLastError();
 }
@@ -590,10 +696,10 @@ MfmaShape mfma_launch_shape(bool balanced, int group_size) {
   return MfmaShape{TILE, balanced ? 1 : waves, IKL_MFMA_PREFETCH + 1};
 }
 
-int mfma_streamk_capacity(int dtype, int head_dim, int group_size) {
+int mfma_streamk_capacity(int dtype, int head_dim, int group_size, bool kv_fp8) {
   const bool bf = dtype == IKL_BF16, two = group_size > 16;
-  if (bf) return two ? capacity_dim<bf16_tag, 2>(head_dim) : capacity_dim<bf16_tag, 1>(head_dim);
-  return two ? capacity_dim<f16_tag, 2>(head_dim) : capacity_dim<f16_tag, 1>(head_dim);
+  if (bf) return two ? capacity_kv<bf16_tag, 2>(head_dim, kv_fp8) : capacity_kv<bf16_tag, 1>(head_dim, kv_fp8);
+  return two ? capacity_kv<f16_tag, 2>(head_dim, kv_fp8) : capacity_kv<f16_tag, 1>(head_dim, kv_fp8);
 }
 
 }  // namespace ikl

@@ -121,7 +121,7 @@ def _validate_attention(query, cache, block_tables, context_lens, layer, validat
         raise ValueError("query head_dim does not match cache layout")
     if query.shape[1] % layout.num_kv_heads != 0:
         raise ValueError("num_heads must be divisible by num_kv_heads")
-    if query.dtype != cache.dtype or query.device != cache.device:
+    if query.dtype != cache.act_dtype or query.device != cache.device:
         raise ValueError("query and cache must have the same dtype and device")
     if block_tables.ndim != 2 or block_tables.shape[0] != query.shape[0]:
         raise ValueError("block_tables must have shape [B, max_blocks]")
@@ -202,8 +202,15 @@ def _attention_args(
     args.partition_size = int(partition_size)
     args.max_context_len = int(max_context_len)
     args.path = int(path)
+    keep = (block_tables, context_lens, k_cache, v_cache)
+    if cache.fp8:
+        ks, vs = cache.k_scale[layer], cache.v_scale[layer]
+        args.cache_dtype = _lib.IKL_FP8_E4M3
+        args.k_scale, args.v_scale = ks.data_ptr(), vs.data_ptr()
+        args.scale_stride_block, args.scale_stride_head = ks.stride(0), ks.stride(1)
+        keep = keep + (ks, vs)
     # keep the tensors whose pointers the struct holds alive with it
-    return args, (block_tables, context_lens, k_cache, v_cache)
+    return args, keep
 
 
 def _launch_attention(
@@ -420,7 +427,7 @@ def append_kv_hip(key: torch.Tensor, value: torch.Tensor, cache, slots: torch.Te
         raise ValueError("slots and key/value token counts must match")
     if not 0 <= layer < layout.num_layers:
         raise IndexError("layer is out of range")
-    if key.dtype != cache.dtype or value.dtype != cache.dtype:
+    if key.dtype != cache.act_dtype or value.dtype != cache.act_dtype:
         raise ValueError("key/value dtype must match the cache dtype")
     if slots.dtype not in _INDEX_TYPES:
         raise ValueError("slots must use int32 or int64")
@@ -466,6 +473,9 @@ def rope_append_kv_hip(query: torch.Tensor | None, key: torch.Tensor, value: tor
                               or query.shape[1] % layout.num_kv_heads != 0):
         raise ValueError("query must have shape [T, H, head_dim] with H a multiple of num_kv_heads")
     tensors = [key, value, cos, sin] + ([query] if query is not None else [])
+    if cache.fp8:
+        raise ValueError("the fused RoPE append writes fp16/bf16/fp32 caches; use rope + append_kv_hip "
+                         "for the FP8 cache")
     if any(x.dtype != cache.dtype for x in tensors):
         raise ValueError("query/key/value/cos/sin must share the cache dtype")
     if any(x.device != cache.device for x in tensors) or slots.device != cache.device:
@@ -528,7 +538,14 @@ def _append_args(key, value, cache, slots, layer):
     args.num_kv_heads = layout.num_kv_heads
     args.head_dim = layout.head_dim
     args.dtype = _DTYPES[key.dtype]
-    return args, (key, value, slots, k_cache, v_cache)
+    keep = (key, value, slots, k_cache, v_cache)
+    if cache.fp8:
+        ks, vs = cache.k_scale[layer], cache.v_scale[layer]
+        args.cache_dtype = _lib.IKL_FP8_E4M3
+        args.k_scale, args.v_scale = ks.data_ptr(), vs.data_ptr()
+        args.scale_stride_block, args.scale_stride_head = ks.stride(0), ks.stride(1)
+        keep = keep + (ks, vs)
+    return args, keep
 
 
 class PreparedPagedAttention:
@@ -607,7 +624,7 @@ class PreparedAppend:
             raise ValueError("slots and key/value token counts must match")
         if slots.dtype not in _INDEX_TYPES:
             raise ValueError("slots must use int32 or int64")
-        if key.dtype != cache.dtype or value.dtype != cache.dtype:
+        if key.dtype != cache.act_dtype or value.dtype != cache.act_dtype:
             raise ValueError("key/value dtype must match the cache dtype")
         if not 0 <= layer < cache.layout.num_layers:
             raise IndexError("layer is out of range")
@@ -694,6 +711,8 @@ class PreparedPagedPrefill:
         batch = len(query_starts)
         self.starts, self.ends = _prefill_ranges(query_starts, context_lens, batch, query_width)
         self.block_tables = _prefill_table(block_tables, cache, batch, self.ends)
+        if cache.fp8:
+            raise ValueError("paged prefill attention reads fp16/bf16/fp32 caches (not the FP8 cache yet)")
         if cache.dtype not in _DTYPES:
             raise ValueError("cache dtype must be float16, bfloat16 or float32")
         self.path = path or paged_prefill_path(dtype=cache.dtype, head_dim=layout.head_dim,

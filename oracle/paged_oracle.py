@@ -17,6 +17,10 @@ It restates, in numpy, the reference's algorithm for this path:
 * ``rope_rows``                  — hf_benchmark.py:69-85 (rotate-half RoPE before the append)
 * ``paged_prefill_attention``    — attention.py:230-321 (gather + causal masked SDPA of a
   ragged prompt-chunk batch)
+* ``e4m3_encode`` / ``e4m3_decode`` / ``quantize_rows_e4m3`` — the FP8 KV format (no
+  counterpart in the reference): OCP E4M3 codes with round-to-nearest-even,
+  saturated to +-448, and one fp32 scale per (token, kv head) row,
+  scale = amax / 448, code = e4m3(x * (448 / amax))
 
 Storage keeps the cache's own element type: float16 and float32 as numpy
 arrays of that type, bfloat16 as raw ``uint16`` bit patterns (numpy has no
@@ -39,7 +43,12 @@ Parity pins (each checked in tests/test_oracle.py):
   attention over its own prefix — the check of the reference's test
   (tests/test_attention.py:90-116), run on that test's tables and ranges —
   plus a float64 causal brute force and torch SDPA under the reference's
-  mask construction (padding rows included).
+  mask construction (padding rows included);
+* e4m3_encode: bit-for-bit against torch's float -> float8_e4m3fn conversion
+  on random values, ties, subnormals, signed zeros and the +-448 ends;
+  e4m3_decode: every one of the 256 codes against torch's decode;
+  quantize_rows_e4m3: closed forms (the row maximum maps to code 0x7e = 448,
+  zero rows keep scale 1, dequantised rows within half an e4m3 step).
 """
 
 from __future__ import annotations
@@ -323,3 +332,54 @@ def brute_force_prefill_f64(query, keys, values, start: int, *, scale=None):
                                                    for vv in values[: pos + 1]], scale=scale)[0])
         out.append(rows)
     return out
+
+
+# ------------------------------------------------------------- FP8 KV format
+E4M3_MAX = 448.0
+
+
+def e4m3_decode(codes: np.ndarray) -> np.ndarray:
+    """OCP E4M3 (e4m3fn) codes -> float32: sign, 4 exponent bits (bias 7), 3
+    mantissa bits; exponent 0 is subnormal (m * 2^-9); 0x7f / 0xff are NaN."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int32)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    e = (c >> 3) & 0xF
+    m = c & 0x7
+    mag = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * 2.0 ** (e - 7))
+    out = (sign * mag).astype(np.float32)
+    out[(c & 0x7F) == 0x7F] = np.nan
+    return out
+
+
+_E4M3_POS = e4m3_decode(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)  # codes 0..0x7e, ascending
+
+
+def e4m3_encode(x: np.ndarray) -> np.ndarray:
+    """float32 -> OCP E4M3 codes, round to nearest (ties to the even code),
+    magnitudes above 448 saturated to 448 (code 0x7e); NaN -> 0x7f."""
+    x = np.asarray(x, dtype=np.float32)
+    a = np.minimum(np.abs(x).astype(np.float64), E4M3_MAX)
+    hi = np.clip(np.searchsorted(_E4M3_POS, a, side="left"), 0, 0x7E)
+    lo = np.clip(hi - 1, 0, 0x7E)
+    d_lo, d_hi = a - _E4M3_POS[lo], _E4M3_POS[hi] - a
+    pick_hi = (d_hi < d_lo) | ((d_hi == d_lo) & (hi % 2 == 0))
+    code = np.where(pick_hi, hi, lo).astype(np.uint8)
+    code = np.where(np.signbit(x), code | 0x80, code).astype(np.uint8)
+    return np.where(np.isnan(x), np.uint8(0x7F), code).astype(np.uint8)
+
+
+def quantize_rows_e4m3(rows: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """[..., D] float rows -> (codes [..., D] uint8, scale [...] float32):
+    amax = max |x| over the row, scale = amax / 448, codes =
+    e4m3(x * (448 / amax)); a zero row keeps scale 1 and codes of x."""
+    x = np.asarray(rows, dtype=np.float32)
+    amax = np.abs(x).max(axis=-1)
+    safe = np.where(amax > 0, amax, np.float32(1.0)).astype(np.float32)
+    scale = np.where(amax > 0, safe / np.float32(E4M3_MAX), np.float32(1.0)).astype(np.float32)
+    inv = np.where(amax > 0, np.float32(E4M3_MAX) / safe, np.float32(1.0)).astype(np.float32)
+    y = np.clip(x * inv[..., None], -E4M3_MAX, E4M3_MAX).astype(np.float32)
+    return e4m3_encode(y), scale
+
+
+def dequantize_rows_e4m3(codes: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    return (e4m3_decode(codes) * np.asarray(scale, np.float32)[..., None]).astype(np.float32)
