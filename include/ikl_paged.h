@@ -34,7 +34,8 @@ extern "C" {
 
 /* Element types of query / cache / key / value / output tensors.
  * IKL_FP8_E4M3 is a cache format only (cache_dtype): OCP E4M3 codes with
- * one fp32 scale per (token, kv head) row, value = decode(code) * scale. */
+ * one power-of-two fp32 scale per (token, kv head) row, value =
+ * decode(code) * scale (exact in fp32, bf16 and fp16). */
 enum ikl_dtype {
   IKL_F16 = 0,
   IKL_BF16 = 1,
@@ -87,10 +88,12 @@ typedef struct ikl_append_args {
   int32_t head_dim;
   int32_t dtype;             /* enum ikl_dtype of key and value (and of the cache unless cache_dtype) */
   /* FP8 KV (no counterpart in the reference): cache_dtype IKL_FP8_E4M3
-   * quantises each appended (token, head) row — scale = amax / 448, codes =
-   * e4m3(x * 448 / amax), round to nearest even, saturating — and writes
-   * the scale to k_scale / v_scale [num_blocks, num_kv_heads, block_size]
-   * fp32 (strides in elements; the token stride is 1). 0 = same as dtype. */
+   * quantises each appended (token, head) row — scale = 2^ceil(log2(amax /
+   * 448)) from the bits of the rounded amax / 448 (at least 2^-126, 1 for a
+   * zero row), codes = e4m3(x / scale), round to nearest even, saturating at
+   * 448 — and writes the scale to k_scale / v_scale [num_blocks,
+   * num_kv_heads, block_size] fp32 (strides in elements; the token stride is
+   * 1). 0 = same as dtype. */
   int32_t cache_dtype;
   void *k_scale;
   void *v_scale;
@@ -183,15 +186,23 @@ typedef struct ikl_rope_append_args {
   int32_t num_heads;         /* 0: rotate and append keys only */
   int32_t num_kv_heads;
   int32_t head_dim;
-  int32_t dtype;             /* enum ikl_dtype of every tensor */
+  int32_t dtype;             /* enum ikl_dtype of every tensor (of the cache unless cache_dtype) */
+  /* FP8 KV cache (cache_dtype IKL_FP8_E4M3; 0 = same as dtype): rope(k) and
+   * v are quantised per (token, head) row as ikl_append_kv does, scales to
+   * k_scale / v_scale [num_blocks, num_kv_heads, block_size]. */
+  int32_t cache_dtype;
+  void *k_scale;
+  void *v_scale;
+  int64_t scale_stride_block, scale_stride_head;
 } ikl_rope_append_args;
 
 /* Rotary embedding + KV append in one launch: query_out = rope(query);
  * cache.k[slot] = rope(key); cache.v[slot] = value; rope(x) = x * cos +
  * rotate_half(x) * sin with rotate_half(x) = [-x2, x1]. Bit-exact with the
  * torch elementwise sequence on the same cos / sin rows (each product and
- * the sum rounded to the tensor dtype). Slots outside the cache are
- * skipped; query rows are rotated regardless. */
+ * the sum rounded to the tensor dtype); into an FP8 cache, equal to that
+ * rotation followed by ikl_append_kv. Slots outside the cache are skipped;
+ * query rows are rotated regardless. */
 int ikl_rope_append_kv(const ikl_rope_append_args *args, void *stream);
 
 /* Arguments of ikl_paged_prefill_attention.
@@ -229,6 +240,12 @@ typedef struct ikl_paged_prefill_args {
   /* Optional hipEvent_t handles recorded on `stream` before [0] and after
    * [1] the attention kernel. NULL entries are skipped. */
   void *events[2];
+  /* FP8 KV cache (cache_dtype IKL_FP8_E4M3; 0 = same as dtype), as in
+   * ikl_paged_attention_args; MFMA kernel only. */
+  int32_t cache_dtype;
+  const void *k_scale;
+  const void *v_scale;
+  int64_t scale_stride_block, scale_stride_head;
 } ikl_paged_prefill_args;
 
 /* Causal prefill attention over the paged cache. Row t of request b sits at

@@ -160,6 +160,11 @@ class RopeAppendArgs(ctypes.Structure):
         ("num_kv_heads", _c_i32),
         ("head_dim", _c_i32),
         ("dtype", _c_i32),
+        ("cache_dtype", _c_i32),
+        ("k_scale", _c_ptr),
+        ("v_scale", _c_ptr),
+        ("scale_stride_block", _c_i64),
+        ("scale_stride_head", _c_i64),
     ]
 
 
@@ -201,6 +206,11 @@ class PagedPrefillArgs(ctypes.Structure):
         ("scale", ctypes.c_float),
         ("path", _c_i32),
         ("events", _c_ptr * 2),
+        ("cache_dtype", _c_i32),
+        ("k_scale", _c_ptr),
+        ("v_scale", _c_ptr),
+        ("scale_stride_block", _c_i64),
+        ("scale_stride_head", _c_i64),
     ]
 
 

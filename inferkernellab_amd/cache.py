@@ -13,8 +13,8 @@ append lives in :mod:`inferkernellab_amd.ops`.
 
 ``dtype=torch.float8_e4m3fn`` selects the FP8 KV format (no counterpart in
 the reference): ``k`` / ``v`` hold OCP E4M3 codes and ``k_scale`` /
-``v_scale`` ``[layers, blocks, kv_heads, block_size]`` one fp32 scale per
-(token, KV head) row; ``act_dtype`` (default bfloat16) is the type of the
+``v_scale`` ``[layers, blocks, kv_heads, block_size]`` one power-of-two
+fp32 scale per (token, KV head) row; ``act_dtype`` (default bfloat16) is the type of the
 rows written into it and of the queries that attend it.
 """
 
@@ -240,18 +240,24 @@ class PagedKVCache:
         return self.k[layer, blocks, offsets], self.v[layer, blocks, offsets]
 
 
+def pow2_scale(amax: torch.Tensor) -> torch.Tensor:
+    """2^ceil(log2(amax / 448)) (at least 2^-126) read off the fp32 bits of
+    amax / 448; 1 where amax is 0 or not finite."""
+    ok = (amax > 0) & torch.isfinite(amax)
+    t = torch.where(ok, amax, torch.full_like(amax, E4M3_MAX)) / torch.full_like(amax, E4M3_MAX)
+    bits = t.view(torch.int32)
+    e = ((bits >> 23) & 0xFF) - 127 + ((bits & 0x7FFFFF) != 0).to(torch.int32)
+    e = e.clamp(-126, 127)
+    scale = ((e + 127) << 23).view(torch.float32)
+    return torch.where(ok, scale, torch.ones_like(scale))
+
+
 def quantize_rows_e4m3(rows: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """[..., D] rows -> (E4M3 codes [..., D], fp32 scales [...]): scale =
-    amax / 448 and codes = e4m3(x * (448 / amax)), saturated to +-448; a zero
-    row keeps scale 1. The HIP append applies the same arithmetic."""
+    """[..., D] rows -> (E4M3 codes [..., D], fp32 scales [...]): a
+    power-of-two scale per row, 2^ceil(log2(amax / 448)), and codes
+    e4m3(x / scale) saturated to +-448. Dividing by a power of two is exact,
+    so the HIP append produces the same codes."""
     x = rows.float()
-    amax = x.abs().amax(dim=-1)
-    nonzero = amax > 0
-    safe = torch.where(nonzero, amax, torch.ones_like(amax))
-    # tensor / tensor: one correctly rounded fp32 division, as the HIP kernel
-    # (a Python scalar over a tensor goes through a reciprocal: two roundings)
-    top = torch.full_like(safe, E4M3_MAX)
-    scale = torch.where(nonzero, safe / top, torch.ones_like(amax))
-    inv = torch.where(nonzero, top / safe, torch.ones_like(amax))
-    codes = (x * inv.unsqueeze(-1)).clamp(-E4M3_MAX, E4M3_MAX).to(FP8_E4M3)
+    scale = pow2_scale(x.abs().amax(dim=-1))
+    codes = (x / scale.unsqueeze(-1)).clamp(-E4M3_MAX, E4M3_MAX).to(FP8_E4M3)
     return codes, scale

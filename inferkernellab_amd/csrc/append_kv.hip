@@ -70,10 +70,9 @@ __global__ __launch_bounds__(256) void append_kv_kernel(AppendParams p) {
 
 // ------------------------------------------------------------ FP8 append
 // One wave per (token, head, K or V) row: lane l converts elements
-// 4l .. 4l+3 (head_dim <= 256). The row maximum gives the scale
-// amax / 448; the codes are e4m3(x * (448 / amax)) clamped to +-448,
-// rounded to nearest even by v_cvt_pk_fp8_f32 (OCP E4M3 on gfx950). A zero
-// row keeps scale 1.
+// 4l .. 4l+3 (head_dim <= 256). The row maximum gives the power-of-two
+// scale e4m3_row_scale(amax); the codes are e4m3(x / scale) clamped to
+// +-448, rounded to nearest even by v_cvt_pk_fp8_f32 (OCP E4M3 on gfx950).
 struct Fp8AppendParams {
   const char *src[2];         // key, value rows
   int64_t src_st[2], src_sh[2];  // bytes
@@ -137,11 +136,10 @@ __global__ __launch_bounds__(64) void append_kv_fp8_kernel(Fp8AppendParams p) {
   float x[4] = {0.f, 0.f, 0.f, 0.f};
   if (on) load4<Tag>(p.src[which] + t * p.src_st[which] + h * p.src_sh[which] + 4 * lane * EB, x);
   const float amax = wave_max(fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))));
-  const float scale = amax > 0.f ? amax / 448.0f : 1.0f;
-  const float inv = amax > 0.f ? 448.0f / amax : 1.0f;
+  const float scale = e4m3_row_scale(amax);
   float y[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) y[i] = fminf(fmaxf(x[i] * inv, -448.0f), 448.0f);
+  for (int i = 0; i < 4; ++i) y[i] = fminf(fmaxf(x[i] / scale, -448.0f), 448.0f);
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w, true);
   if (on) *reinterpret_cast<int *>(p.dst[which] + blk * p.dst_sb[which] + off * p.dst_st[which] + h * p.dst_sh[which] + 4 * lane) = w;

@@ -161,6 +161,18 @@ __device__ inline uint32_t u32x4_at(const u32x4 &v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
 
+// FP8 KV rows: the power-of-two scale 2^ceil(log2(amax / 448)) (at least
+// 2^-126) of a row whose largest magnitude is amax, read off the bits of the
+// correctly rounded amax / 448; 1 for a zero or non-finite amax. Codes are
+// e4m3(x / scale): the division by a power of two is exact.
+__device__ inline float e4m3_row_scale(float amax) {
+  if (!(amax > 0.f) || amax == INFINITY) return 1.0f;
+  const uint32_t bits = __float_as_uint(amax / 448.0f);
+  int e = (int)((bits >> 23) & 0xffu) - 127 + ((bits & 0x7fffffu) != 0u ? 1 : 0);
+  e = e < -126 ? -126 : (e > 127 ? 127 : e);
+  return __uint_as_float((uint32_t)(e + 127) << 23);
+}
+
 template <typename IdxT>
 __device__ inline int64_t load_index(const void *base, int64_t i) {
   return (int64_t)(reinterpret_cast<const IdxT *>(base)[i]);

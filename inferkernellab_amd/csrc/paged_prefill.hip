@@ -68,6 +68,12 @@ struct PrefillParams {
   int32_t table_i64;
   int32_t idx_i64;   // starts / lens element type
   float scale_log2;  // scale * log2(e)
+  // FP8 KV cache: E4M3 codes, one fp32 scale per (token, head) row in
+  // k_scale / v_scale [blocks, kv heads, block_size]
+  int32_t kv_fp8;
+  const float *k_scale;
+  const float *v_scale;
+  int64_t s_sb, s_sh;  // elements
 };
 
 namespace {
@@ -125,7 +131,25 @@ constexpr int PWAVES = 4;  // waves per workgroup
 #define IKL_PREFILL_PRIO 0  // bit 0: raise wave priority over the QK^T MFMAs; bit 1: over PV
 #endif
 
-template <typename Tag, int D, int NG>
+// Two E4M3 codes times one fp32 scale -> two 16-bit values (one rounding).
+template <typename Tag>
+__device__ inline uint32_t fp8x2_scaled(uint32_t w, float scale, bool hi);
+template <>
+__device__ inline uint32_t fp8x2_scaled<bf16_tag>(uint32_t w, float scale, bool hi) {
+  return __builtin_bit_cast(uint32_t, hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, scale, true)
+                                        : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, scale, false));
+}
+template <>
+__device__ inline uint32_t fp8x2_scaled<f16_tag>(uint32_t w, float scale, bool hi) {
+  return __builtin_bit_cast(uint32_t, hi ? __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, scale, true)
+                                        : __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, scale, false));
+}
+
+// KV8: the cache holds E4M3 codes with per-row scales. The copy waves load
+// the codes (half the bytes) and each row's scale, and stage
+// round(code * scale) in the same 16-bit tile layout, so the tile loop is
+// unchanged.
+template <typename Tag, int D, int NG, bool KV8>
 __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_prefill_mfma_kernel(const PrefillParams p) {
   static_assert(D % 32 == 0 && D <= 128, "MFMA prefill needs head_dim = 32k <= 128");
   using ops = mfma_ops<Tag>;
@@ -139,8 +163,10 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
   constexpr int RWG = RW * PWAVES;           // query rows per workgroup
   constexpr int TILE_BYTES = PT * ROWB;      // one staged K or V tile
   constexpr int PF = IKL_PREFILL_PREFETCH;   // tiles fetched ahead
-  constexpr int PPL = 16 * PIECES / 64;      // copy pieces per lane (a wave moves a half tile)
-  static_assert(PWAVES == 4 && (16 * PIECES) % 64 == 0, "four waves copy K / V halves");
+  constexpr int CEB = KV8 ? 1 : EB;          // bytes per cache element
+  constexpr int CPIECES = D * CEB / 16;      // 16-byte pieces per cache row
+  constexpr int PPL = (16 * CPIECES + 63) / 64;  // copy pieces per lane (a wave moves a half tile)
+  static_assert(PWAVES == 4 && (KV8 || (16 * PIECES) % 64 == 0), "four waves copy K / V halves");
   // row rotations of the staged K and V tiles (bijective per row)
   auto kswz = [](int row) { return (row & 3) + 4 * (row >> 3); };
   auto vswz = [](int row) { return 2 * (row & 3) + 8 * ((row >> 3) & 1); };
@@ -229,18 +255,27 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
   // or V (w >= 2), PPL 16-byte pieces per lane, so each wave resolves one
   // block and builds one buffer resource per tile.
   const int cp_v = wave >> 1, cp_h = wave & 1;
-  const int row_bytes = (int)((cp_v ? p.v_st : p.k_st) * EB);
-  const char *cp_base = (cp_v ? p.vc + (int64_t)kvh * p.v_sh * EB : p.kc + (int64_t)kvh * p.k_sh * EB);
+  const int row_bytes = (int)((cp_v ? p.v_st : p.k_st) * CEB);
+  const char *cp_base = (cp_v ? p.vc + (int64_t)kvh * p.v_sh * CEB : p.kc + (int64_t)kvh * p.k_sh * CEB);
   const int64_t cp_sb = cp_v ? p.v_sb : p.k_sb, cp_st = cp_v ? p.v_st : p.k_st;
-  int cp_off[PPL], cp_lds[PPL];
+  const char *cp_scale = KV8 ? (const char *)(cp_v ? p.v_scale : p.k_scale) + (int64_t)kvh * p.s_sh * 4 : nullptr;
+  // piece u of this lane: cache piece c of half-row r; staged (16-bit)
+  // pieces sp .. sp + (KV8 ? 1 : 0) of tile row 16 cp_h + r
+  int cp_off[PPL], cp_lds[PPL], cp_lds2[PPL], cp_row[PPL];
+  bool cp_ok[PPL];
 #pragma unroll
   for (int u = 0; u < PPL; ++u) {
-    const int pi = u * 64 + lane, r = pi / PIECES, c = pi % PIECES;
-    const int row = 16 * cp_h + r;
-    cp_off[u] = r * row_bytes + c * 16;
-    cp_lds[u] = row * ROWB + ((c + (cp_v ? vswz(row) : kswz(row))) % PIECES) * 16;
+    const int pi = u * 64 + lane, r = pi / CPIECES, c = pi % CPIECES;
+    const int row = 16 * cp_h + (r < 16 ? r : 15);
+    const int sw = cp_v ? vswz(row) : kswz(row);
+    const int sp = KV8 ? 2 * c : c;
+    cp_ok[u] = pi < 16 * CPIECES;
+    cp_row[u] = r < 16 ? r : 15;
+    cp_off[u] = cp_row[u] * row_bytes + c * 16;
+    cp_lds[u] = row * ROWB + ((sp + sw) % PIECES) * 16;
+    cp_lds2[u] = row * ROWB + ((sp + 1 + sw) % PIECES) * 16;
   }
-  const char *vbase = p.vc + (int64_t)kvh * p.v_sh * EB;
+  const char *vbase = p.vc + (int64_t)kvh * p.v_sh * CEB;
 
   // Block ids: a window of 64 table entries, one per lane, read with
   // v_readlane (no memory access per tile).
@@ -252,6 +287,7 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
   // the tile's keys in blocks inside the cache.
   struct Staged {
     v4u32 d[PPL];
+    float sc[PPL];  // KV8: the scale of each piece's row
     uint32_t blocks;
   };
 
@@ -276,11 +312,20 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
     const int left = end - pos;
     const int nv = ph < 0 || left <= 0 ? 0 : (left < 16 ? left : 16);
     const int64_t blk = ph < 0 ? 0 : ph;
+    const int64_t in_blk = pos - (int64_t)lb * p.block_size;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(cp_base + (blk * cp_sb + (int64_t)(pos - lb * p.block_size) * cp_st) * EB), (short)0,
-        nv * row_bytes, 0x00020000);
+        (void *)(cp_base + (blk * cp_sb + in_blk * cp_st) * CEB), (short)0, nv * row_bytes, 0x00020000);
 #pragma unroll
-    for (int u = 0; u < PPL; ++u) T.d[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, cp_off[u], 0, 0);
+    for (int u = 0; u < PPL; ++u)
+      if (cp_ok[u]) T.d[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, cp_off[u], 0, 0);
+    if constexpr (KV8) {
+      // the half's 16 row scales (rows past nv read as 0)
+      const __amdgpu_buffer_rsrc_t ss = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)(cp_scale + (blk * p.s_sb + in_blk) * 4), (short)0, nv * 4, 0x00020000);
+#pragma unroll
+      for (int u = 0; u < PPL; ++u)
+        if (cp_ok[u]) T.sc[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ss, cp_row[u] * 4, 0, 0));
+    }
   };
 
   // Row sums of P on the matrix cores: ones[16 x 32] . P gives every row
@@ -391,7 +436,21 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
     char *vt = lds[j & 1][1];
     char *mine = cp_v ? vt : kt;
 #pragma unroll
-    for (int u = 0; u < PPL; ++u) *reinterpret_cast<v4u32 *>(mine + cp_lds[u]) = T.d[u];
+    for (int u = 0; u < PPL; ++u) {
+      if (!cp_ok[u]) continue;
+      if constexpr (KV8) {
+        const v4u32 w = T.d[u];
+        const float sc = T.sc[u];
+        *reinterpret_cast<v4u32 *>(mine + cp_lds[u]) =
+            v4u32{fp8x2_scaled<Tag>(w.x, sc, false), fp8x2_scaled<Tag>(w.x, sc, true),
+                  fp8x2_scaled<Tag>(w.y, sc, false), fp8x2_scaled<Tag>(w.y, sc, true)};
+        *reinterpret_cast<v4u32 *>(mine + cp_lds2[u]) =
+            v4u32{fp8x2_scaled<Tag>(w.z, sc, false), fp8x2_scaled<Tag>(w.z, sc, true),
+                  fp8x2_scaled<Tag>(w.w, sc, false), fp8x2_scaled<Tag>(w.w, sc, true)};
+      } else {
+        *reinterpret_cast<v4u32 *>(mine + cp_lds[u]) = T.d[u];
+      }
+    }
     const uint32_t mask = T.blocks;
     __syncthreads();
     if (j + PF < n_tiles) fetch(j + PF, T);
@@ -416,7 +475,8 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
 #pragma unroll
   for (int g = 0; g < NG; ++g) lsum[g] = lacc[g][0];
   const int ph_first = pf_block(p, b, 0);
-  const char *v0row = ph_first >= 0 && end > 0 ? vbase + (int64_t)ph_first * p.v_sb * EB : nullptr;
+  const char *v0row = ph_first >= 0 && end > 0 ? vbase + (int64_t)ph_first * p.v_sb * CEB : nullptr;
+  const float v0scale = KV8 && v0row ? p.v_scale[(int64_t)ph_first * p.s_sb + (int64_t)kvh * p.s_sh] : 0.f;
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
     const int64_t r = wr0 + 16 * g + hl;
@@ -437,7 +497,14 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
 #pragma unroll
       for (int mt = 0; mt < MTILES; ++mt) {
         u32x2_t w = u32x2_t{0u, 0u};
-        if (v0row) w = *reinterpret_cast<const u32x2_t *>(v0row + (16 * mt + 4 * grp) * EB);
+        if (v0row) {
+          if constexpr (KV8) {
+            const uint32_t c = *reinterpret_cast<const uint32_t *>(v0row + 16 * mt + 4 * grp);
+            w = u32x2_t{fp8x2_scaled<Tag>(c, v0scale, false), fp8x2_scaled<Tag>(c, v0scale, true)};
+          } else {
+            w = *reinterpret_cast<const u32x2_t *>(v0row + (16 * mt + 4 * grp) * EB);
+          }
+        }
         *reinterpret_cast<u32x2_t *>(dst + 32 * mt) = w;
       }
     }
@@ -558,13 +625,13 @@ __global__ __launch_bounds__(64) void paged_prefill_scalar_kernel(const PrefillP
   }
 }
 
-template <typename Tag, int NG>
+template <typename Tag, int NG, bool KV8>
 hipError_t launch_mfma_dim(int d, const PrefillParams &p, dim3 grid, hipStream_t s) {
   switch (d) {
-    case 32: paged_prefill_mfma_kernel<Tag, 32, NG><<<grid, 64 * PWAVES, 0, s>>>(p); break;
-    case 64: paged_prefill_mfma_kernel<Tag, 64, NG><<<grid, 64 * PWAVES, 0, s>>>(p); break;
-    case 96: paged_prefill_mfma_kernel<Tag, 96, NG><<<grid, 64 * PWAVES, 0, s>>>(p); break;
-    default: paged_prefill_mfma_kernel<Tag, 128, NG><<<grid, 64 * PWAVES, 0, s>>>(p); break;
+    case 32: paged_prefill_mfma_kernel<Tag, 32, NG, KV8><<<grid, 64 * PWAVES, 0, s>>>(p); break;
+    case 64: paged_prefill_mfma_kernel<Tag, 64, NG, KV8><<<grid, 64 * PWAVES, 0, s>>>(p); break;
+    case 96: paged_prefill_mfma_kernel<Tag, 96, NG, KV8><<<grid, 64 * PWAVES, 0, s>>>(p); break;
+    default: paged_prefill_mfma_kernel<Tag, 128, NG, KV8><<<grid, 64 * PWAVES, 0, s>>>(p); break;
   }
   return hipGetLastError();
 }
@@ -605,8 +672,17 @@ extern "C" int ikl_paged_prefill_attention(const ikl_paged_prefill_args *a, void
   if (a->table_width > (int64_t(1) << 40) / a->block_size)
     return fail(IKL_EINVAL, "ikl_paged_prefill_attention: table_width * block_size is too large");
 
+  if (a->cache_dtype != 0 && a->cache_dtype != a->dtype && a->cache_dtype != IKL_FP8_E4M3)
+    return fail(IKL_EINVAL, "ikl_paged_prefill_attention: cache_dtype must be 0, the query dtype or IKL_FP8_E4M3");
+  const bool kv8 = a->cache_dtype == IKL_FP8_E4M3;
   const int auto_path = ikl_paged_prefill_path(a->dtype, a->head_dim, a->block_size);
   const int path = a->path < 0 ? auto_path : a->path;
+  if (kv8 && path != IKL_PATH_MFMA_GROUPED)
+    return fail(IKL_EUNSUPPORTED, "ikl_paged_prefill_attention: the FP8 cache is read by the MFMA kernel only "
+                                  "(fp16/bf16 queries, head_dim 32/64/96/128, block size a multiple of 16)");
+  if (kv8 && (!a->k_scale || !a->v_scale || ((uintptr_t)a->k_scale & 3u) || ((uintptr_t)a->v_scale & 3u)))
+    return fail(IKL_EINVAL, "ikl_paged_prefill_attention: the FP8 cache needs aligned k_scale / v_scale");
+  const int ceb = kv8 ? 1 : eb;  // cache bytes per element
   if (path != IKL_PATH_MFMA_GROUPED && path != IKL_PATH_SCALAR_GROUPED)
     return fail(IKL_EINVAL, "ikl_paged_prefill_attention: path must be -1, IKL_PATH_SCALAR_GROUPED or IKL_PATH_MFMA_GROUPED");
   if (path == IKL_PATH_MFMA_GROUPED && auto_path != IKL_PATH_MFMA_GROUPED)
@@ -615,7 +691,7 @@ extern "C" int ikl_paged_prefill_attention(const ikl_paged_prefill_args *a, void
     // 32-bit positions and 32-bit byte offsets inside a 16-row half tile
     if (a->table_width * a->block_size >= (int64_t(1) << 31) - 64)
       return fail(IKL_EINVAL, "ikl_paged_prefill_attention: table_width * block_size must stay below 2^31");
-    if (16 * a->k_stride_token * eb >= (int64_t(1) << 31) || 16 * a->v_stride_token * eb >= (int64_t(1) << 31) ||
+    if (16 * a->k_stride_token * ceb >= (int64_t(1) << 31) || 16 * a->v_stride_token * ceb >= (int64_t(1) << 31) ||
         a->k_stride_token < a->head_dim || a->v_stride_token < a->head_dim)
       return fail(IKL_EINVAL, "ikl_paged_prefill_attention: token strides must lie in [head_dim, 2^27)");
   }
@@ -623,10 +699,13 @@ extern "C" int ikl_paged_prefill_attention(const ikl_paged_prefill_args *a, void
   // every row the kernels touch must be aligned to its access width
   const int64_t align = path == IKL_PATH_MFMA_GROUPED ? 16 : 4;
   const int64_t out_align = path == IKL_PATH_MFMA_GROUPED ? 8 : 4;
-  const int64_t in_strides[] = {a->q_stride_b, a->q_stride_h, a->q_stride_t, a->k_stride_block, a->k_stride_token,
-                                a->k_stride_head, a->v_stride_block, a->v_stride_token, a->v_stride_head};
-  for (int64_t st : in_strides)
+  const int64_t q_strides[] = {a->q_stride_b, a->q_stride_h, a->q_stride_t};
+  for (int64_t st : q_strides)
     if ((st * eb) % align != 0) return fail(IKL_EINVAL, "ikl_paged_prefill_attention: misaligned input stride");
+  const int64_t c_strides[] = {a->k_stride_block, a->k_stride_token, a->k_stride_head,
+                               a->v_stride_block, a->v_stride_token, a->v_stride_head};
+  for (int64_t st : c_strides)
+    if ((st * ceb) % align != 0) return fail(IKL_EINVAL, "ikl_paged_prefill_attention: misaligned input stride");
   const int64_t out_strides[] = {a->out_stride_b, a->out_stride_h, a->out_stride_t};
   for (int64_t st : out_strides)
     if ((st * eb) % out_align != 0) return fail(IKL_EINVAL, "ikl_paged_prefill_attention: misaligned output stride");
@@ -670,6 +749,11 @@ extern "C" int ikl_paged_prefill_attention(const ikl_paged_prefill_args *a, void
   p.idx_i64 = a->lens_type == IKL_I64;
   const float scale = a->scale > 0.f ? a->scale : 1.f / sqrtf((float)a->head_dim);
   p.scale_log2 = scale * LOG2E;
+  p.kv_fp8 = kv8 ? 1 : 0;
+  p.k_scale = (const float *)a->k_scale;
+  p.v_scale = (const float *)a->v_scale;
+  p.s_sb = a->scale_stride_block;
+  p.s_sh = a->scale_stride_head;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipEvent_t ev0 = static_cast<hipEvent_t>(a->events[0]), ev1 = static_cast<hipEvent_t>(a->events[1]);
@@ -684,8 +768,12 @@ extern "C" int ikl_paged_prefill_attention(const ikl_paged_prefill_args *a, void
     const int64_t blocks = p.row_blocks * p.bh_pad;
     if (blocks > 0x7fffffffLL) return fail(IKL_EINVAL, "ikl_paged_prefill_attention: launch too large");
     const dim3 grid((unsigned)blocks);
-    if (a->dtype == IKL_BF16) err = launch_mfma_dim<bf16_tag, NG>(a->head_dim, p, grid, s);
-    else err = launch_mfma_dim<f16_tag, NG>(a->head_dim, p, grid, s);
+    if (a->dtype == IKL_BF16)
+      err = p.kv_fp8 ? launch_mfma_dim<bf16_tag, NG, true>(a->head_dim, p, grid, s)
+                     : launch_mfma_dim<bf16_tag, NG, false>(a->head_dim, p, grid, s);
+    else
+      err = p.kv_fp8 ? launch_mfma_dim<f16_tag, NG, true>(a->head_dim, p, grid, s)
+                     : launch_mfma_dim<f16_tag, NG, false>(a->head_dim, p, grid, s);
   } else {
     const int64_t blocks = a->batch * a->num_heads * a->query_width;
     if (blocks > 0x7fffffffLL) return fail(IKL_EINVAL, "ikl_paged_prefill_attention: launch too large");

@@ -156,6 +156,159 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeParams p) {
   }
 }
 
+// ------------------------------------------------------ into an FP8 cache
+// One wave per row of a token: q rows (rotated), k rows (rotated, then
+// quantised) and v rows (quantised). Lane l takes elements 4l .. 4l+3 of
+// the first half and their rotate-half partners 4l + D/2 ..; the k / v row
+// maximum gives the power-of-two scale e4m3_row_scale(amax) and codes
+// e4m3(x / scale), as ikl_append_kv does for rows that arrive already
+// rotated.
+struct RopeFp8Params {
+  RopeParams r;  // kc / vc strides in bytes (= elements)
+  float *k_scale;
+  float *v_scale;
+  int64_t s_sb, s_sh;  // elements
+  int32_t head_dim;
+};
+
+template <typename Tag>
+struct four;
+template <>
+struct four<bf16_tag> {
+  static constexpr int BYTES = 8;
+  __device__ static inline void load(const char *p, float *x) {
+    const uint2 w = *reinterpret_cast<const uint2 *>(p);
+    x[0] = elem<bf16_tag>::lo(w.x);
+    x[1] = elem<bf16_tag>::hi(w.x);
+    x[2] = elem<bf16_tag>::lo(w.y);
+    x[3] = elem<bf16_tag>::hi(w.y);
+  }
+  __device__ static inline void store(char *p, const float *x) {
+    *reinterpret_cast<uint2 *>(p) = uint2{elem<bf16_tag>::pack2(x[0], x[1]), elem<bf16_tag>::pack2(x[2], x[3])};
+  }
+};
+template <>
+struct four<f16_tag> {
+  static constexpr int BYTES = 8;
+  __device__ static inline void load(const char *p, float *x) {
+    const uint2 w = *reinterpret_cast<const uint2 *>(p);
+    x[0] = elem<f16_tag>::lo(w.x);
+    x[1] = elem<f16_tag>::hi(w.x);
+    x[2] = elem<f16_tag>::lo(w.y);
+    x[3] = elem<f16_tag>::hi(w.y);
+  }
+  __device__ static inline void store(char *p, const float *x) {
+    *reinterpret_cast<uint2 *>(p) = uint2{elem<f16_tag>::pack2(x[0], x[1]), elem<f16_tag>::pack2(x[2], x[3])};
+  }
+};
+template <>
+struct four<f32_tag> {
+  static constexpr int BYTES = 16;
+  __device__ static inline void load(const char *p, float *x) {
+    const float4 w = *reinterpret_cast<const float4 *>(p);
+    x[0] = w.x;
+    x[1] = w.y;
+    x[2] = w.z;
+    x[3] = w.w;
+  }
+  __device__ static inline void store(char *p, const float *x) {
+    *reinterpret_cast<float4 *>(p) = float4{x[0], x[1], x[2], x[3]};
+  }
+};
+
+__device__ inline float wave_max_abs(float v) {
+  v = fmaxf(v, dpp_mov<DPP_QUAD_XOR1>(v));
+  v = fmaxf(v, dpp_mov<DPP_QUAD_XOR2>(v));
+  v = fmaxf(v, dpp_mov<DPP_ROW_HALF_MIRROR>(v));
+  v = fmaxf(v, dpp_mov<DPP_ROW_MIRROR>(v));
+  return max_xor32(max_xor16(v));
+}
+
+// Quantises 8 values (lo[4] at element 4l, hi[4] at 4l + D/2) of a row whose
+// wave-wide maximum magnitude is amax; writes codes and (lane 0) the scale.
+__device__ inline void store_fp8_row(char *dst, float *scale_dst, int lane, int half, bool on, const float *lo,
+                                     const float *hi, float amax) {
+  const float scale = e4m3_row_scale(amax);
+  float y[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    y[i] = fminf(fmaxf(lo[i] / scale, -448.0f), 448.0f);
+    y[4 + i] = fminf(fmaxf(hi[i] / scale, -448.0f), 448.0f);
+  }
+  int wl = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+  wl = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], wl, true);
+  int wh = __builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], 0, false);
+  wh = __builtin_amdgcn_cvt_pk_fp8_f32(y[6], y[7], wh, true);
+  if (on) {
+    *reinterpret_cast<int *>(dst + 4 * lane) = wl;
+    *reinterpret_cast<int *>(dst + half + 4 * lane) = wh;
+  }
+  if (lane == 0) *scale_dst = scale;
+}
+
+template <typename Tag, typename IdxT>
+__global__ __launch_bounds__(64) void rope_append_fp8_kernel(RopeFp8Params f) {
+  using M = rope_math<Tag>;
+  using F = four<Tag>;
+  constexpr int EB = F::BYTES / 4;
+  const RopeParams &p = f.r;
+  const int lane = threadIdx.x;
+  const int row = blockIdx.x;  // q rows, then k rows, then v rows
+  const int64_t t = blockIdx.y;
+  const int half = f.head_dim / 2;
+  const bool on = 4 * lane < half;
+  const int64_t slot = (int64_t)reinterpret_cast<const IdxT *>(p.slots)[t];
+  const bool slot_ok = slot >= 0 && slot < p.num_slots;
+  const int64_t blk = slot_ok ? slot / p.block_size : 0;
+  const int64_t off = slot_ok ? slot - blk * p.block_size : 0;
+  if (row >= p.num_heads && !slot_ok) return;
+  const int kv_row = row - p.num_heads;
+  float a[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
+  if (kv_row >= p.num_kv_heads) {  // v row: quantise as is
+    const int h = kv_row - p.num_kv_heads;
+    const char *src = p.value + t * p.v_st + h * p.v_sh;
+    if (on) {
+      F::load(src + 4 * lane * EB, a);
+      F::load(src + (half + 4 * lane) * EB, b);
+    }
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(a[i]), fabsf(b[i])));
+    store_fp8_row(p.vc + blk * p.vc_sb + off * p.vc_st + h * p.vc_sh, f.v_scale + blk * f.s_sb + h * f.s_sh + off,
+                  lane, half, on, a, b, wave_max_abs(m));
+    return;
+  }
+  // rotate a q or k row
+  const char *src = row < p.num_heads ? p.q_in + t * p.qi_st + row * p.qi_sh : p.key + t * p.k_st + kv_row * p.k_sh;
+  float x1[4] = {0.f, 0.f, 0.f, 0.f}, x2[4] = {0.f, 0.f, 0.f, 0.f}, c1[4], c2[4], s1[4], s2[4];
+  if (on) {
+    F::load(src + 4 * lane * EB, x1);
+    F::load(src + (half + 4 * lane) * EB, x2);
+    F::load(p.cos + t * p.cos_st + 4 * lane * EB, c1);
+    F::load(p.cos + t * p.cos_st + (half + 4 * lane) * EB, c2);
+    F::load(p.sin + t * p.sin_st + 4 * lane * EB, s1);
+    F::load(p.sin + t * p.sin_st + (half + 4 * lane) * EB, s2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[i] = M::add(M::mul(x1[i], c1[i]), M::mul(-x2[i], s1[i]));  // x1 cos - x2 sin
+      b[i] = M::add(M::mul(x2[i], c2[i]), M::mul(x1[i], s2[i]));   // x2 cos + x1 sin
+    }
+  }
+  if (row < p.num_heads) {
+    if (on) {
+      char *dst = p.q_out + t * p.qo_st + row * p.qo_sh;
+      F::store(dst + 4 * lane * EB, a);
+      F::store(dst + (half + 4 * lane) * EB, b);
+    }
+    return;
+  }
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(a[i]), fabsf(b[i])));
+  store_fp8_row(p.kc + blk * p.kc_sb + off * p.kc_st + kv_row * p.kc_sh,
+                f.k_scale + blk * f.s_sb + kv_row * f.s_sh + off, lane, half, on, a, b, wave_max_abs(m));
+}
+
 template <typename Tag>
 void launch_rope(const RopeParams &p, int64_t tokens, bool i64, hipStream_t s) {
   if (i64) rope_append_kernel<Tag, int64_t><<<dim3((unsigned)tokens), 256, 0, s>>>(p);
@@ -189,9 +342,16 @@ extern "C" int ikl_rope_append_kv(const ikl_rope_append_args *a, void *stream) {
     case IKL_F32: eb = 4; break;
     default: return fail(IKL_EINVAL, "rope append: unsupported dtype");
   }
+  const bool fp8 = a->cache_dtype == IKL_FP8_E4M3;
+  if (a->cache_dtype != 0 && a->cache_dtype != a->dtype && !fp8)
+    return fail(IKL_EINVAL, "rope append: cache_dtype must be 0, the tensor dtype or IKL_FP8_E4M3");
   const int64_t row = (int64_t)a->head_dim * eb;
   if (row % 32 != 0)
     return fail(IKL_EUNSUPPORTED, "rope append: head_dim * element size must be a multiple of 32 bytes");
+  if (fp8 && (a->head_dim % 8 != 0 || a->head_dim > 512))
+    return fail(IKL_EUNSUPPORTED, "rope append: the FP8 cache needs head_dim a multiple of 8, at most 512");
+  if (fp8 && (!a->k_scale || !a->v_scale)) return fail(IKL_EINVAL, "rope append: the FP8 cache needs k_scale and v_scale");
+  const int ceb = fp8 ? 1 : eb;  // cache bytes per element
   RopeParams p;
   p.q_in = (const char *)a->query;
   p.q_out = (char *)a->query_out;
@@ -212,12 +372,12 @@ extern "C" int ikl_rope_append_kv(const ikl_rope_append_args *a, void *stream) {
   p.slots = a->slots;
   p.kc = (char *)a->k_cache;
   p.vc = (char *)a->v_cache;
-  p.kc_sb = a->k_stride_block * eb;
-  p.kc_st = a->k_stride_token * eb;
-  p.kc_sh = a->k_stride_head * eb;
-  p.vc_sb = a->v_stride_block * eb;
-  p.vc_st = a->v_stride_token * eb;
-  p.vc_sh = a->v_stride_head * eb;
+  p.kc_sb = a->k_stride_block * ceb;
+  p.kc_st = a->k_stride_token * ceb;
+  p.kc_sh = a->k_stride_head * ceb;
+  p.vc_sb = a->v_stride_block * ceb;
+  p.vc_st = a->v_stride_token * ceb;
+  p.vc_sh = a->v_stride_head * ceb;
   p.num_slots = a->num_blocks * (int64_t)a->block_size;
   p.block_size = a->block_size;
   p.num_heads = a->num_heads;
@@ -232,6 +392,34 @@ extern "C" int ikl_rope_append_kv(const ikl_rope_append_args *a, void *stream) {
   if (!ok) return fail(IKL_EINVAL, "rope append: rows must be 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
   const bool i64 = a->slot_type == IKL_I64;
+  if (fp8) {
+    if (((uintptr_t)a->k_scale & 3u) || ((uintptr_t)a->v_scale & 3u))
+      return fail(IKL_EINVAL, "rope append: misaligned scale tensor");
+    if ((int64_t)a->num_heads + 2 * (int64_t)a->num_kv_heads > 0x7fffffffLL)
+      return fail(IKL_EINVAL, "rope append: too many heads");
+    RopeFp8Params f;
+    f.r = p;
+    f.k_scale = (float *)a->k_scale;
+    f.v_scale = (float *)a->v_scale;
+    f.s_sb = a->scale_stride_block;
+    f.s_sh = a->scale_stride_head;
+    f.head_dim = a->head_dim;
+    const dim3 grid((unsigned)(a->num_heads + 2 * a->num_kv_heads), (unsigned)a->num_tokens);
+#define IKL_ROPE8(TAG)                                                                  \
+  do {                                                                                  \
+    if (i64) rope_append_fp8_kernel<TAG, int64_t><<<grid, 64, 0, s>>>(f);               \
+    else rope_append_fp8_kernel<TAG, int32_t><<<grid, 64, 0, s>>>(f);                   \
+  } while (0)
+    switch (a->dtype) {
+      case IKL_F16: IKL_ROPE8(f16_tag); break;
+      case IKL_BF16: IKL_ROPE8(bf16_tag); break;
+      default: IKL_ROPE8(f32_tag); break;
+    }
+#undef IKL_ROPE8
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(IKL_ELAUNCH, std::string("rope append launch: ") + hipGetErrorString(e));
+    return IKL_OK;
+  }
   switch (a->dtype) {
     case IKL_F16: launch_rope<f16_tag>(p, a->num_tokens, i64, s); break;
     case IKL_BF16: launch_rope<bf16_tag>(p, a->num_tokens, i64, s); break;

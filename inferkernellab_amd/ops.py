@@ -473,10 +473,7 @@ def rope_append_kv_hip(query: torch.Tensor | None, key: torch.Tensor, value: tor
                               or query.shape[1] % layout.num_kv_heads != 0):
         raise ValueError("query must have shape [T, H, head_dim] with H a multiple of num_kv_heads")
     tensors = [key, value, cos, sin] + ([query] if query is not None else [])
-    if cache.fp8:
-        raise ValueError("the fused RoPE append writes fp16/bf16/fp32 caches; use rope + append_kv_hip "
-                         "for the FP8 cache")
-    if any(x.dtype != cache.dtype for x in tensors):
+    if any(x.dtype != cache.act_dtype for x in tensors):
         raise ValueError("query/key/value/cos/sin must share the cache dtype")
     if any(x.device != cache.device for x in tensors) or slots.device != cache.device:
         raise ValueError("tensors must be on the cache device")
@@ -511,7 +508,12 @@ def rope_append_kv_hip(query: torch.Tensor | None, key: torch.Tensor, value: tor
     a.k_stride_block, a.k_stride_token, a.k_stride_head = kc.stride(0), kc.stride(1), kc.stride(2)
     a.v_stride_block, a.v_stride_token, a.v_stride_head = vc.stride(0), vc.stride(1), vc.stride(2)
     a.num_tokens, a.num_blocks, a.block_size = t, layout.num_blocks, layout.block_size
-    a.num_kv_heads, a.head_dim, a.dtype = layout.num_kv_heads, layout.head_dim, _DTYPES[cache.dtype]
+    a.num_kv_heads, a.head_dim, a.dtype = layout.num_kv_heads, layout.head_dim, _DTYPES[cache.act_dtype]
+    if cache.fp8:
+        ks, vs = cache.k_scale[layer], cache.v_scale[layer]
+        a.cache_dtype = _lib.IKL_FP8_E4M3
+        a.k_scale, a.v_scale = ks.data_ptr(), vs.data_ptr()
+        a.scale_stride_block, a.scale_stride_head = ks.stride(0), ks.stride(1)
     with torch.cuda.device(key.device):
         stream = torch.cuda.current_stream(key.device).cuda_stream
         status = lib.ikl_rope_append_kv(ctypes.byref(a), ctypes.c_void_p(stream))
@@ -711,12 +713,13 @@ class PreparedPagedPrefill:
         batch = len(query_starts)
         self.starts, self.ends = _prefill_ranges(query_starts, context_lens, batch, query_width)
         self.block_tables = _prefill_table(block_tables, cache, batch, self.ends)
-        if cache.fp8:
-            raise ValueError("paged prefill attention reads fp16/bf16/fp32 caches (not the FP8 cache yet)")
-        if cache.dtype not in _DTYPES:
+        if cache.act_dtype not in _DTYPES:
             raise ValueError("cache dtype must be float16, bfloat16 or float32")
-        self.path = path or paged_prefill_path(dtype=cache.dtype, head_dim=layout.head_dim,
+        self.path = path or paged_prefill_path(dtype=cache.act_dtype, head_dim=layout.head_dim,
                                                block_size=layout.block_size)
+        if cache.fp8 and self.path != "mfma_grouped":
+            raise ValueError("the FP8 cache is read by the MFMA prefill kernel only (fp16/bf16, head_dim "
+                             "32/64/96/128, block size a multiple of 16)")
         if self.path not in ("mfma_grouped", "scalar_grouped"):
             raise ValueError("path must be 'mfma_grouped' or 'scalar_grouped'")
         self._row_align = 16 if self.path == "mfma_grouped" else 4
@@ -740,7 +743,8 @@ class PreparedPagedPrefill:
         a.num_blocks = layout.num_blocks
         a.num_heads, a.num_kv_heads = num_heads, layout.num_kv_heads
         a.head_dim, a.block_size = layout.head_dim, layout.block_size
-        a.dtype = _DTYPES[cache.dtype]
+        a.dtype = _DTYPES[cache.act_dtype]
+        a.cache_dtype = _lib.IKL_FP8_E4M3 if cache.fp8 else 0
         a.scale = float(scale if scale is not None else layout.head_dim**-0.5)
         a.path = _PATH_IDS[self.path]
         self._args = a
@@ -753,7 +757,7 @@ class PreparedPagedPrefill:
         layout = self.cache.layout
         if tuple(query.shape) != self.shape:
             raise ValueError(f"query must have shape {list(self.shape)}")
-        if query.dtype != self.cache.dtype or query.device != self.cache.device:
+        if query.dtype != self.cache.act_dtype or query.device != self.cache.device:
             raise ValueError("query and cache must have the same dtype and device")
         if not 0 <= layer < layout.num_layers:
             raise IndexError("layer is out of range")
@@ -773,6 +777,10 @@ class PreparedPagedPrefill:
         a.v_stride_block, a.v_stride_token, a.v_stride_head = vc.stride()[:3]
         a.out = out.data_ptr()
         a.out_stride_b, a.out_stride_h, a.out_stride_t = out.stride(0), out.stride(1), out.stride(2)
+        if self.cache.fp8:
+            ks, vs = self.cache.k_scale[layer], self.cache.v_scale[layer]
+            a.k_scale, a.v_scale = ks.data_ptr(), vs.data_ptr()
+            a.scale_stride_block, a.scale_stride_head = ks.stride(0), ks.stride(1)
         for i in range(2):
             a.events[i] = events[i] if events is not None else None
         with torch.cuda.device(query.device):

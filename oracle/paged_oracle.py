@@ -19,8 +19,8 @@ It restates, in numpy, the reference's algorithm for this path:
   ragged prompt-chunk batch)
 * ``e4m3_encode`` / ``e4m3_decode`` / ``quantize_rows_e4m3`` — the FP8 KV format (no
   counterpart in the reference): OCP E4M3 codes with round-to-nearest-even,
-  saturated to +-448, and one fp32 scale per (token, kv head) row,
-  scale = amax / 448, code = e4m3(x * (448 / amax))
+  saturated to +-448, and one power-of-two fp32 scale per (token, kv head)
+  row, scale = 2^ceil(log2(amax / 448)), code = e4m3(x / scale)
 
 Storage keeps the cache's own element type: float16 and float32 as numpy
 arrays of that type, bfloat16 as raw ``uint16`` bit patterns (numpy has no
@@ -47,8 +47,9 @@ Parity pins (each checked in tests/test_oracle.py):
 * e4m3_encode: bit-for-bit against torch's float -> float8_e4m3fn conversion
   on random values, ties, subnormals, signed zeros and the +-448 ends;
   e4m3_decode: every one of the 256 codes against torch's decode;
-  quantize_rows_e4m3: closed forms (the row maximum maps to code 0x7e = 448,
-  zero rows keep scale 1, dequantised rows within half an e4m3 step).
+  quantize_rows_e4m3: closed forms (power-of-two scales, the row maximum
+  lands in (224, 448], zero rows keep scale 1, dequantised rows within half
+  an e4m3 step).
 """
 
 from __future__ import annotations
@@ -368,16 +369,27 @@ def e4m3_encode(x: np.ndarray) -> np.ndarray:
     return np.where(np.isnan(x), np.uint8(0x7F), code).astype(np.uint8)
 
 
+def pow2_scale(amax: np.ndarray) -> np.ndarray:
+    """Power-of-two scale of rows with maximum magnitude amax:
+    2^ceil(log2(t)) for t = amax / 448 (one correctly rounded fp32 division),
+    read off t's bits (at least 2^-126); 1 for amax == 0 or non-finite."""
+    amax = np.asarray(amax, dtype=np.float32)
+    ok = (amax > 0) & np.isfinite(amax)
+    t = np.where(ok, amax, np.float32(448)).astype(np.float32) / np.float32(E4M3_MAX)
+    bits = t.astype(np.float32).view(np.int32)
+    e = ((bits >> 23) & 0xFF) - 127 + ((bits & 0x7FFFFF) != 0)
+    e = np.clip(e, -126, 127)
+    scale = ((e + 127).astype(np.int32) << 23).view(np.float32)
+    return np.where(ok, scale, np.float32(1.0)).astype(np.float32)
+
+
 def quantize_rows_e4m3(rows: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """[..., D] float rows -> (codes [..., D] uint8, scale [...] float32):
-    amax = max |x| over the row, scale = amax / 448, codes =
-    e4m3(x * (448 / amax)); a zero row keeps scale 1 and codes of x."""
+    scale = pow2_scale(max |x| over the row), codes = e4m3(x / scale), an
+    exact scaling (a power of two) followed by one rounding."""
     x = np.asarray(rows, dtype=np.float32)
-    amax = np.abs(x).max(axis=-1)
-    safe = np.where(amax > 0, amax, np.float32(1.0)).astype(np.float32)
-    scale = np.where(amax > 0, safe / np.float32(E4M3_MAX), np.float32(1.0)).astype(np.float32)
-    inv = np.where(amax > 0, np.float32(E4M3_MAX) / safe, np.float32(1.0)).astype(np.float32)
-    y = np.clip(x * inv[..., None], -E4M3_MAX, E4M3_MAX).astype(np.float32)
+    scale = pow2_scale(np.abs(x).max(axis=-1))
+    y = np.clip(x / scale[..., None], -E4M3_MAX, E4M3_MAX).astype(np.float32)
     return e4m3_encode(y), scale
 
 

@@ -176,3 +176,31 @@ def test_fp8_cache_is_rejected_where_not_supported():
                               max_context_len=None, path=ops._PATH_IDS["scalar_grouped"])
     with pytest.raises(ValueError, match="query and cache"):
         ops.paged_decode_attention_hip_grouped(q.half(), cache, tables, lens)
+
+
+@pytest.mark.parametrize("act", ["bfloat16", "float16"])
+@pytest.mark.parametrize("heads,kv,dim,bs,starts,ends,width", [
+    (32, 8, 128, 16, [0, 40, 300], [77, 200, 420], 160),
+    (16, 4, 96, 32, [0, 5], [130, 70], 130),
+    (8, 8, 64, 16, [3, 0], [40, 19], 40),
+    (32, 1, 32, 48, [0, 60], [100, 100], 100),
+])
+def test_fp8_prefill_attention_matches_oracle(act, heads, kv, dim, bs, starts, ends, width):
+    """The MFMA prefill kernel over an FP8 cache against the oracle's prefill
+    attention on the dequantised cache (padding rows: the value at position
+    0, rounded to the query dtype)."""
+    from inferkernellab_amd import PreparedPagedPrefill
+
+    base, packed = _fp8_case(batch=len(ends), heads=heads, kv=kv, dim=dim, bs=bs, lengths=ends, act=act,
+                             seed=dim + bs)
+    cache = _device_fp8_cache(base, packed, act)
+    gen = torch.Generator().manual_seed(dim)
+    q = randn_storage(gen, (len(ends), heads, width, dim), act)
+    prep = PreparedPagedPrefill(cache, base.device_tables(), starts, ends, num_heads=heads, query_width=width)
+    assert prep.path == "mfma_grouped"
+    got = prep(storage_to_torch(q, act).cuda(), 0)
+    torch.cuda.synchronize()
+    exp = po.paged_prefill_attention(po.to_f32(q, act), base.oracle_cache, base.tables, starts, ends)
+    out = got.float().cpu().numpy()
+    assert not np.isnan(out).any()
+    assert float(np.max(np.abs(out - exp))) < ATOL[act]

@@ -72,3 +72,56 @@ def test_rope_append_skips_slots_outside_the_cache():
 
 def test_rope_append_prefill_sized_batch():
     _run("bfloat16", tokens=2048, heads=16, kv=4, num_blocks=200)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_rope_append_into_fp8_cache_equals_rope_then_fp8_append(dtype, head_dim):
+    """Into the FP8 cache the fused kernel equals ikl_rope_append_kv's own
+    rotation followed by ikl_append_kv's quantisation: rotated q, codes and
+    scales bit for bit, slots outside the cache skipped."""
+    from inferkernellab_amd import ops
+    from inferkernellab_amd.cache import PagedKVCache
+    from inferkernellab_amd.llama import RotaryEmbedding
+
+    print(f"rope append fp8 {dtype} D={head_dim}", flush=True)
+    tokens, heads, kv, bs, nb = 23, 16, 4, 16, 12
+    gen = torch.Generator().manual_seed(head_dim)
+    tdt = getattr(torch, dtype)
+    q = torch.randn(tokens, heads, head_dim, generator=gen).to(tdt).cuda()
+    k = (torch.randn(tokens, kv, head_dim, generator=gen) * 4).to(tdt).cuda()
+    v = torch.randn(tokens, kv, head_dim, generator=gen).to(tdt).cuda()
+    pos = torch.randint(0, 3000, (tokens,), generator=gen).cuda()
+    cos, sin = RotaryEmbedding(head_dim, 10000.0).cuda()(q, pos.view(-1, 1))
+    cos, sin = cos[:, 0].contiguous().to(tdt), sin[:, 0].contiguous().to(tdt)
+    slots = torch.randperm(nb * bs, generator=gen)[:tokens].to(torch.int32)
+    slots[4] = -1
+    slots[9] = nb * bs
+    slots = slots.cuda()
+
+    fused = PagedKVCache(nb, bs, kv, head_dim, dtype=torch.float8_e4m3fn, act_dtype=tdt, device="cuda")
+    for t in (fused.k.view(torch.uint8), fused.v.view(torch.uint8)):
+        t.fill_(0x11)
+    q_fused = ops.rope_append_kv_hip(q.clone(), k, v, cos, sin, fused, slots)
+
+    # reference: the same rotation into a 16-bit cache, then the FP8 append of its rows
+    plain = PagedKVCache(nb, bs, kv, head_dim, dtype=tdt, device="cuda")
+    plain.k.zero_()
+    q_plain = ops.rope_append_kv_hip(q.clone(), k, v, cos, sin, plain, slots)
+    k_rot = plain.k[0].reshape(nb * bs, kv, head_dim)
+    ok = (slots >= 0) & (slots < nb * bs)
+    good = slots[ok].long()
+    sep = PagedKVCache(nb, bs, kv, head_dim, dtype=torch.float8_e4m3fn, act_dtype=tdt, device="cuda")
+    for t in (sep.k.view(torch.uint8), sep.v.view(torch.uint8)):
+        t.fill_(0x11)
+    ops.append_kv_hip(k_rot[good].contiguous(), v[ok].contiguous(), sep, slots[ok].contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(q_fused.view(torch.uint8) if tdt != torch.float32 else q_fused,
+                       q_plain.view(torch.uint8) if tdt != torch.float32 else q_plain)
+    assert torch.equal(fused.k.view(torch.uint8), sep.k.view(torch.uint8))
+    assert torch.equal(fused.v.view(torch.uint8), sep.v.view(torch.uint8))
+    flat_ok = torch.zeros(nb * bs, dtype=torch.bool, device="cuda")
+    flat_ok[good] = True
+    written = flat_ok.view(nb, bs)
+    for a, b in ((fused.k_scale[0], sep.k_scale[0]), (fused.v_scale[0], sep.v_scale[0])):
+        assert torch.equal(a.transpose(1, 2)[written], b.transpose(1, 2)[written])
