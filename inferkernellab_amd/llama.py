@@ -218,7 +218,7 @@ class LlamaPagedDecodeRunner:
                  max_num_batched_tokens: int = 2048, prefill_mode: str = "batched",
                  temperature: float = 0.0, top_p: float = 1.0, seed: int = 2026,
                  eos_token_ids: Sequence[int] | None = None, use_graph: bool = True,
-                 prefill_attention: str = "hip") -> None:
+                 prefill_attention: str = "hip", kv_cache_dtype: torch.dtype | None = None) -> None:
         if not prompts:
             raise ValueError("at least one prompt is required")
         if max_new_tokens <= 0:
@@ -262,8 +262,16 @@ class LlamaPagedDecodeRunner:
         self.prompt_lengths = tuple(len(p) for p in self.prompts)
         width = max(-(-(n + max_new_tokens) // block_size) for n in self.prompt_lengths)
         total_blocks = sum(-(-(n + max_new_tokens) // block_size) for n in self.prompt_lengths)
+        # kv_cache_dtype=torch.float8_e4m3fn: the FP8 KV format (E4M3 codes,
+        # one power-of-two scale per token and head) under fp16/bf16 models
+        fp8 = kv_cache_dtype == torch.float8_e4m3fn
+        if kv_cache_dtype not in (None, self.dtype) and not fp8:
+            raise ValueError("kv_cache_dtype must be None, the model dtype or torch.float8_e4m3fn")
+        if fp8 and self.dtype not in (torch.float16, torch.bfloat16):
+            raise ValueError("the FP8 KV cache needs an fp16 or bf16 model")
         self.cache = PagedKVCache(total_blocks, block_size, self.num_kv_heads, self.head_dim,
-                                  num_layers=self.num_layers, dtype=self.dtype, device=self.device)
+                                  num_layers=self.num_layers, dtype=kv_cache_dtype if fp8 else self.dtype,
+                                  act_dtype=self.dtype if fp8 else None, device=self.device)
         batched = prefill_mode == "batched"
         self.runtime = InferenceRuntime(
             self.cache,
@@ -352,6 +360,9 @@ class LlamaPagedDecodeRunner:
         blocks = tables[:, kpos // bs].to(torch.long)
         k = self.cache.k[layer][blocks, kpos % bs]  # [B, L, Hkv, D]
         v = self.cache.v[layer][blocks, kpos % bs]
+        if self.cache.fp8:  # dequantise: codes times their row scales
+            k = k.float() * self.cache.k_scale[layer][blocks, :, kpos % bs].unsqueeze(-1)
+            v = v.float() * self.cache.v_scale[layer][blocks, :, kpos % bs].unsqueeze(-1)
         end_t = torch.tensor(list(ends), device=self.device).view(b, 1)
         start_t = torch.tensor(list(starts), device=self.device).view(b, 1)
         kvalid = kpos.view(1, -1) < end_t  # [B, L]

@@ -404,7 +404,7 @@ def paged_decode_attention_hip_grouped(
         query_group_size=1 if heads_per_kv == 1 else query_group_size,
         partition_size=partition_size,
         max_context_len=max_context_len,
-        path=_PATH_IDS[path_name],
+        path=-1 if cache.fp8 else _PATH_IDS[path_name],  # the FP8 cache is read by the MFMA family only
     )
 
 

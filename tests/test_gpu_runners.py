@@ -215,6 +215,32 @@ def test_llama_hip_prefill_matches_torch_prefix_attention(dtype, tol):
         assert float((a.float() - b.float()).abs().max()) <= 2 * tol * scale
 
 
+def test_llama_fp8_kv_cache_matches_its_torch_path_and_stays_near_bf16():
+    """kv_cache_dtype=float8_e4m3fn: the HIP path (fused RoPE append into the
+    FP8 cache, FP8 prefill and decode kernels) against the runner's torch
+    path over the same quantised cache (torch quantiser + dequantised fp32
+    prefix attention), and the FP8 run's logits near the bf16-cache run."""
+    from inferkernellab_amd.llama import LlamaPagedDecodeRunner
+
+    cfg, model = _llama(torch.bfloat16, hidden_size=512, intermediate_size=512, num_attention_heads=8,
+                        num_key_value_heads=2, vocab_size=256, num_hidden_layers=2)
+    gen = np.random.default_rng(11)
+    prompts = [gen.integers(0, 256, size=n).tolist() for n in (70, 33, 5)]
+    kw = dict(max_new_tokens=4, block_size=16, max_num_batched_tokens=48)
+    fp8 = LlamaPagedDecodeRunner(model, prompts, kv_cache_dtype=torch.float8_e4m3fn, **kw).run()
+    ref = LlamaPagedDecodeRunner(model, prompts, kv_cache_dtype=torch.float8_e4m3fn, prefill_attention="torch",
+                                 append_backend="torch", **kw).run()
+    bf16 = LlamaPagedDecodeRunner(model, prompts, **kw).run()
+    scale = float(ref.prompt_logits.float().abs().max())
+    err = float((fp8.prompt_logits.float() - ref.prompt_logits.float()).abs().max())
+    assert err <= 3e-2 * scale, (err, scale)
+    for a, b in zip(fp8.decode_logits, ref.decode_logits):
+        assert float((a.float() - b.float()).abs().max()) <= 6e-2 * scale
+    q_err = float((fp8.prompt_logits.float() - bf16.prompt_logits.float()).abs().max())
+    print(f"FP8 vs bf16 KV cache: prompt logits max abs diff {q_err:.4f} (logit scale {scale:.3f})")
+    assert q_err <= 0.15 * scale
+
+
 def test_llama_sampling_is_seeded_and_eos_stops():
     from inferkernellab_amd.llama import LlamaPagedDecodeRunner
 
