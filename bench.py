@@ -83,7 +83,7 @@ class HipEvents:
         self.lib.hipEventDestroy(ctypes.c_void_p(handle))
 
 
-def build_workload(name: str, device: torch.device, seed: int = 0):
+def build_workload(name: str, device: torch.device, seed: int = 0, head_major: bool | None = None):
     from inferkernellab_amd import PagedKVCache
 
     batch, heads, kv_heads, head_dim, dtype, lo, hi, pool, kv_scale, _ = WORKLOADS[name][:10]
@@ -105,7 +105,7 @@ def build_workload(name: str, device: torch.device, seed: int = 0):
         from inferkernellab_amd.cache import quantize_rows_e4m3
 
         cache = PagedKVCache(pool, block_size, kv_heads, head_dim, dtype=torch.float8_e4m3fn, act_dtype=dtype,
-                             device=device)
+                             device=device, head_major=head_major)
         step = 1024  # blocks quantised per chunk
         for codes, scales in ((cache.k, cache.k_scale), (cache.v, cache.v_scale)):
             for b0 in range(0, pool, step):
@@ -115,7 +115,8 @@ def build_workload(name: str, device: torch.device, seed: int = 0):
                 codes[0, b0 : b0 + n] = c
                 scales[0, b0 : b0 + n] = sc.transpose(1, 2)
     else:
-        cache = PagedKVCache(pool, block_size, kv_heads, head_dim, dtype=dtype, device=device)
+        cache = PagedKVCache(pool, block_size, kv_heads, head_dim, dtype=dtype, device=device,
+                             head_major=head_major)
         for t in (cache.k, cache.v):
             t.normal_(0.0, kv_scale, generator=dgen)
     query = torch.randn(batch, heads, head_dim, generator=dgen, device=device, dtype=torch.float32).to(dtype)
@@ -455,6 +456,9 @@ def main() -> int:
     parser.add_argument("--cpu-budget-s", type=float, default=15.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--seed", type=int, default=0)
+    parser.add_argument("--kv-layout", choices=("default", "token-major", "head-major"), default="default",
+                        help="cache block layout: [block_size, kv_heads, D] (the reference's, default for "
+                             "16-bit caches) or [kv_heads, block_size, D] (default for the FP8 cache)")
     parser.add_argument("--no-graph", action="store_true",
                         help="time eager launches instead of HIP graph replays of the step")
     parser.add_argument("--copy-calibration", action="store_true",
@@ -487,7 +491,8 @@ def main() -> int:
 
     from inferkernellab_amd import ops
 
-    w = build_workload(args.workload, device, args.seed)
+    head_major = {"default": None, "token-major": False, "head-major": True}[args.kv_layout]
+    w = build_workload(args.workload, device, args.seed, head_major=head_major)
     partition = args.partition_size or WORKLOADS[args.workload][9]
     attn = ops.PreparedPagedAttention(
         w["query"], w["cache"], w["tables"], w["lens"], validate_inputs=True,
@@ -587,6 +592,7 @@ def main() -> int:
             "num_blocks": w["pool"],
             "context_tokens": sum(w["lengths"]),
             "kv_cache": "fp8 e4m3 codes + one fp32 scale per (token, kv head)" if w["fp8"] else "same as dtype",
+            "kv_block_layout": "[kv_heads, block_size, D]" if w["cache"].head_major else "[block_size, kv_heads, D]",
             "partition_size": attn.partition_size,
             "split": "balanced (equal tile runs per resident wave)" if attn.balanced_split
                      else f"fixed partitions of {attn.partition_size} tokens",

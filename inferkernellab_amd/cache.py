@@ -112,13 +112,26 @@ class PagedKVCache:
         dtype: torch.dtype = torch.float16,
         device: torch.device | str = "cpu",
         act_dtype: torch.dtype | None = None,
+        head_major: bool | None = None,
     ):
         if min(num_layers, num_blocks, block_size, num_kv_heads, head_dim) <= 0:
             raise ValueError("cache dimensions must be positive")
         self.layout = CacheLayout(num_layers, num_blocks, block_size, num_kv_heads, head_dim)
-        shape = (num_layers, num_blocks, block_size, num_kv_heads, head_dim)
-        self.k = torch.empty(shape, dtype=dtype, device=torch.device(device))
-        self.v = torch.empty_like(self.k)
+        # head_major stores each block as [kv_heads, block_size, head_dim], so the
+        # rows of one head are contiguous; k / v stay [layers, blocks,
+        # block_size, kv_heads, head_dim] views either way (the kernels take
+        # strides). The reference's layout (token-major) is the default; the
+        # FP8 format, which no caller shares with the reference, is head-major.
+        self.head_major = (dtype == FP8_E4M3) if head_major is None else bool(head_major)
+        dev = torch.device(device)
+        if self.head_major:
+            store = (num_layers, num_blocks, num_kv_heads, block_size, head_dim)
+            self.k = torch.empty(store, dtype=dtype, device=dev).transpose(2, 3)
+            self.v = torch.empty(store, dtype=dtype, device=dev).transpose(2, 3)
+        else:
+            shape = (num_layers, num_blocks, block_size, num_kv_heads, head_dim)
+            self.k = torch.empty(shape, dtype=dtype, device=dev)
+            self.v = torch.empty_like(self.k)
         self.device = self.k.device
         self.allocator = BlockAllocator(num_blocks)
         self.fp8 = dtype == FP8_E4M3

@@ -700,6 +700,12 @@ extern "C" int ikl_paged_attention(const ikl_paged_attention_args *a, void *stre
       a->v_stride_token % cvec || a->v_stride_head % cvec || a->out_stride_b % vec ||
       a->out_stride_h % vec)
     return fail(IKL_EINVAL, "attention: query/cache/out rows must be 16-byte aligned");
+  // the MFMA family addresses the rows of a 16-token tile through 32-bit byte offsets
+  if (pl.path == IKL_PATH_MFMA_GROUPED &&
+      (16 * a->k_stride_token * (pl.kv_fp8 ? 1 : pl.eb) >= (int64_t(1) << 31) ||
+       16 * a->v_stride_token * (pl.kv_fp8 ? 1 : pl.eb) >= (int64_t(1) << 31) ||
+       a->k_stride_token < a->head_dim || a->v_stride_token < a->head_dim))
+    return fail(IKL_EINVAL, "attention: token strides must lie in [head_dim, 2^27 bytes / 16)");
   if (pl.kv_fp8 && (!a->k_scale || !a->v_scale || !aligned16(a->k_scale) || !aligned16(a->v_scale) ||
                     a->scale_stride_block % 4 || a->scale_stride_head % 4))
     return fail(IKL_EINVAL, "attention: the FP8 cache needs 16-byte aligned k_scale / v_scale rows");

@@ -54,9 +54,14 @@ constexpr int TILE = 16;  // tokens per tile
 #endif
 
 // bf16 P with its rounding residual in a second MFMA (fp16 P is not split).
-template <typename Tag>
+// The FP8 cache skips it: its values carry 4 significant bits, far below
+// what the residual would add.
+#ifndef IKL_MFMA_SPLIT_P_FP8
+#define IKL_MFMA_SPLIT_P_FP8 0
+#endif
+template <typename Tag, bool KV8 = false>
 constexpr bool split_p() {
-  return IKL_MFMA_SPLIT_P != 0 && mfma_ops<Tag>::NARROW_P;
+  return (KV8 ? IKL_MFMA_SPLIT_P_FP8 : IKL_MFMA_SPLIT_P) != 0 && mfma_ops<Tag>::NARROW_P;
 }
 
 // Two E4M3 codes -> two bf16 / fp16 values (exact: every E4M3 value is a
@@ -314,7 +319,7 @@ struct WaveTiles {
         // A bf16 P keeps 8 significant bits; with SPLIT_P its rounding
         // residual P - bf16(P) goes through a second MFMA, so P enters with
         // ~16 bits (as the fp32 P of the reference's kernels).
-        if constexpr (split_p<Tag>())
+        if constexpr (split_p<Tag, KV8>())
           pl[g] = u32x2_t{ops::pack(pr[0] - ops::lo(pb[g].x), pr[1] - ops::hi(pb[g].x)),
                           ops::pack(pr[2] - ops::lo(pb[g].y), pr[3] - ops::hi(pb[g].y))};
       }
@@ -327,7 +332,7 @@ struct WaveTiles {
         for (int g = 0; g < NG; ++g)
           acc[g][mt] = ops::mma_k16(__builtin_bit_cast(u32x2_t, va[mt]), pb[g], acc[g][mt]);
       }
-      if constexpr (split_p<Tag>()) {
+      if constexpr (split_p<Tag, KV8>()) {
 #pragma unroll
         for (int mt = 0; mt < MTILES; ++mt)
 #pragma unroll
