@@ -127,9 +127,6 @@ constexpr int PWAVES = 4;  // waves per workgroup
 #define IKL_PREFILL_MIN_WAVES 2
 #endif
 #define IKL_PREFILL_WAVES_ATTR __attribute__((amdgpu_waves_per_eu(IKL_PREFILL_MIN_WAVES, 8)))
-#ifndef IKL_PREFILL_PRIO
-#define IKL_PREFILL_PRIO 0  // bit 0: raise wave priority over the QK^T MFMAs; bit 1: over PV
-#endif
 
 // Two E4M3 codes times one fp32 scale -> two 16-bit values (one rounding).
 template <typename Tag>
@@ -225,12 +222,15 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
     for (int s = 0; s < KSTEPS; ++s) asm volatile("" ::"v"(qb[g][s]));
 
   f32x4_t acc[NG][MTILES];
-  float m[NG];  // running max of each lane's row, log2 domain (scaled)
+  float m[NG];    // running max of each lane's row, log2 domain (scaled)
+  float thr[NG];  // (m + RESCALE_LOG2) in raw score units (scale > 0)
+  const float inv_scale_log2 = 1.f / p.scale_log2;
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
 #pragma unroll
     for (int mt = 0; mt < MTILES; ++mt) acc[g][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     m[g] = NEG_SENTINEL;
+    thr[g] = NEG_SENTINEL;
   }
 
   // LDS offsets. The 16-byte pieces of a staged row are rotated by a
@@ -277,18 +277,41 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
   }
   const char *vbase = p.vc + (int64_t)kvh * p.v_sh * CEB;
 
-  // Block ids: a window of 64 table entries, one per lane, read with
-  // v_readlane (no memory access per tile).
-  int win_base = 0;
-  int win = pf_block(p, b, lane);
-  asm volatile("" ::"v"(win));  // in registers before the tile loop starts
+  // The block table as a window of 64 consecutive 16-key halves, one per
+  // lane: the byte offset of the half's first row from the wave's cache base
+  // (and, for FP8, of its first row scale), plus a bit of `holes` for each
+  // half whose block lies outside the cache. A tile reads its offsets with
+  // v_readlane and its hole bits with a scalar shift, so the per-tile block
+  // lookup is a handful of scalar instructions; the window moves every 32
+  // tiles (block_size % 16 == 0: a half never straddles two blocks).
+  const int64_t cp_blk_bytes = cp_sb * CEB, cp_row_bytes = cp_st * CEB;
+  int hbase = 0;
+  uint32_t woff_lo, woff_hi, wsc_lo = 0, wsc_hi = 0;
+  uint64_t holes_w;
+  auto load_window = [&](int h0) {
+    const uint32_t pos = 16u * (uint32_t)(h0 + lane);
+    const uint32_t lb = pos / (uint32_t)p.block_size;
+    const int ph = pf_block(p, b, lb);
+    const int64_t in_blk = pos - (int64_t)lb * p.block_size;
+    const int64_t off = ph >= 0 ? ph * cp_blk_bytes + in_blk * cp_row_bytes : 0;
+    woff_lo = (uint32_t)off;
+    woff_hi = (uint32_t)((uint64_t)off >> 32);
+    if constexpr (KV8) {
+      const int64_t so = ph >= 0 ? (ph * p.s_sb + in_blk) * 4 : 0;
+      wsc_lo = (uint32_t)so;
+      wsc_hi = (uint32_t)((uint64_t)so >> 32);
+    }
+    holes_w = __builtin_amdgcn_ballot_w64(ph < 0);
+    asm volatile("" ::"v"(woff_lo), "v"(woff_hi));  // in registers before the tiles that read them
+  };
+  load_window(0);
 
-  // Register staging of the copy (PF tiles in flight), with the bitmask of
-  // the tile's keys in blocks inside the cache.
+  // Register staging of the copy (PF tiles in flight), with the tile's hole
+  // bits (bit h: half h lies in a block outside the cache).
   struct Staged {
     v4u32 d[PPL];
     float sc[PPL];  // KV8: the scale of each piece's row
-    uint32_t blocks;
+    uint32_t holes;
   };
 
   // Global -> registers for tile j into T. The half is one block window
@@ -297,31 +320,26 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
   // read as zero without a branch. Keys past the end need no other mask:
   // they lie past every row's causal limit.
   auto fetch = [&](int j, Staged &T) {
-    const int pos0 = j * PT;
-    const int lb0 = p.bs_shift >= 0 ? (pos0 >> p.bs_shift) : pos0 / p.block_size;
-    const int lb1 = p.bs_shift >= 0 ? ((pos0 + 16) >> p.bs_shift) : (pos0 + 16) / p.block_size;
-    if (lb1 - win_base >= 64) {
-      win_base = lb0;
-      win = pf_block(p, b, (int64_t)win_base + lane);
-      asm volatile("" ::"v"(win));
+    const int h0 = 2 * j;
+    if (h0 + 1 - hbase >= 64) {
+      hbase = h0;
+      load_window(hbase);
     }
-    const int ph0 = __builtin_amdgcn_readlane(win, lb0 - win_base);
-    const int ph1 = __builtin_amdgcn_readlane(win, lb1 - win_base);
-    T.blocks = (ph0 >= 0 ? 0xffffu : 0u) | (ph1 >= 0 ? 0xffff0000u : 0u);
-    const int ph = cp_h ? ph1 : ph0, lb = cp_h ? lb1 : lb0, pos = pos0 + 16 * cp_h;
-    const int left = end - pos;
-    const int nv = ph < 0 || left <= 0 ? 0 : (left < 16 ? left : 16);
-    const int64_t blk = ph < 0 ? 0 : ph;
-    const int64_t in_blk = pos - (int64_t)lb * p.block_size;
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(cp_base + (blk * cp_sb + in_blk * cp_st) * CEB), (short)0, nv * row_bytes, 0x00020000);
+    const int i0 = h0 - hbase, i = i0 + cp_h;
+    T.holes = (uint32_t)(holes_w >> i0) & 3u;
+    const uint64_t off = ((uint64_t)__builtin_amdgcn_readlane(woff_hi, i) << 32) | __builtin_amdgcn_readlane(woff_lo, i);
+    const int left = end - 16 * (h0 + cp_h);
+    const int nv = (T.holes >> cp_h) & 1u ? 0 : (left <= 0 ? 0 : (left < 16 ? left : 16));
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(cp_base + off), (short)0, nv * row_bytes, 0x00020000);
 #pragma unroll
     for (int u = 0; u < PPL; ++u)
       if (cp_ok[u]) T.d[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, cp_off[u], 0, 0);
     if constexpr (KV8) {
       // the half's 16 row scales (rows past nv read as 0)
-      const __amdgpu_buffer_rsrc_t ss = __builtin_amdgcn_make_buffer_rsrc(
-          (void *)(cp_scale + (blk * p.s_sb + in_blk) * 4), (short)0, nv * 4, 0x00020000);
+      const uint64_t so = ((uint64_t)__builtin_amdgcn_readlane(wsc_hi, i) << 32) | __builtin_amdgcn_readlane(wsc_lo, i);
+      const __amdgpu_buffer_rsrc_t ss =
+          __builtin_amdgcn_make_buffer_rsrc((void *)(cp_scale + so), (short)0, nv * 4, 0x00020000);
 #pragma unroll
       for (int u = 0; u < PPL; ++u)
         if (cp_ok[u]) T.sc[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ss, cp_row[u] * 4, 0, 0));
@@ -336,10 +354,10 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
   for (int g = 0; g < NG; ++g) lacc[g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const v4u32 ones = v4u32{ops::ONE2, ops::ONE2, ops::ONE2, ops::ONE2};
 
-  auto compute = [&](const char *kt, const char *vt, int base, uint32_t blocks) {
+  auto compute = [&](const char *kt, const char *vt, int base, uint32_t holes_t) {
     if (base >= w_hi) return;                  // no row of this wave reaches the tile
     const bool causal = base + PT - 1 > w_lo;  // diagonal tile: per-key causal test
-    const bool holes = blocks != 0xffffffffu;  // keys in blocks outside the cache
+    const bool holes = holes_t != 0u;          // keys in blocks outside the cache
     v4u32 ka[2][KSTEPS];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -348,9 +366,6 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
     // every group's S^T first, so one group's softmax overlaps the next
     // group's MFMAs
     f32x4_t s0[NG], s1[NG];
-#if IKL_PREFILL_PRIO & 1
-    __builtin_amdgcn_s_setprio(1);
-#endif
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       s0[g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -361,9 +376,6 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
         s1[g] = ops::mma_k32(ka[1][s], qb[g][s], s1[g]);
       }
     }
-#if IKL_PREFILL_PRIO & 1
-    __builtin_amdgcn_s_setprio(0);
-#endif
     v4u32 pb[NG], pl[NG];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
@@ -381,16 +393,23 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
         for (int j = 0; j < 8; ++j) sc[j] = j <= lim ? sc[j] : -INFINITY;
       }
       if (holes) {
+        // the lane's 8 keys lie in half grp / 2
+        const bool dead = (holes_t >> (grp >> 1)) & 1u;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) sc[j] = (blocks >> (8 * grp + j)) & 1u ? sc[j] : -INFINITY;
+        for (int j = 0; j < 8; ++j) sc[j] = dead ? -INFINITY : sc[j];
       }
-      float tmax = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
-                         fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
-      tmax = max_xor32(max_xor16(tmax)) * p.scale_log2;
-      const bool need = tmax > m[g] + RESCALE_LOG2;
-      if (__builtin_amdgcn_ballot_w64(need) != 0ull) {
+      // Lazy rescale: the row maximum is only needed when a score passes
+      // m + RESCALE_LOG2 (scaled), and each lane can test its own 8 scores
+      // against that bound in raw units, so the cross-lane reduction runs
+      // on those tiles only (the first one and rare growth).
+      const float lmax = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
+                               fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+      if (__builtin_amdgcn_ballot_w64(lmax > thr[g]) != 0ull) {
+        const float tmax = max_xor32(max_xor16(lmax)) * p.scale_log2;
+        const bool need = tmax > m[g] + RESCALE_LOG2;
         const float alpha = need ? fast_exp2(m[g] - tmax) : 1.f;
         m[g] = need ? tmax : m[g];
+        thr[g] = (m[g] + RESCALE_LOG2) * inv_scale_log2;
         lacc[g] *= alpha;
 #pragma unroll
         for (int mt = 0; mt < MTILES; ++mt) acc[g][mt] *= alpha;
@@ -410,9 +429,6 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
         lacc[g] = ops::mma_k32(ones, pl[g], lacc[g]);
       }
     }
-#if IKL_PREFILL_PRIO & 2
-    __builtin_amdgcn_s_setprio(1);
-#endif
 #pragma unroll
     for (int mt = 0; mt < MTILES; ++mt) {
       const u32x2_t v0 = lds_read_tr(vt + tr_off[0][mt]), v1 = lds_read_tr(vt + tr_off[1][mt]);
@@ -423,17 +439,10 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
         if constexpr (SPLIT) acc[g][mt] = ops::mma_k32(va, pl[g], acc[g][mt]);
       }
     }
-#if IKL_PREFILL_PRIO & 2
-    __builtin_amdgcn_s_setprio(0);
-#endif
   };
 
-  // Tile j: registers -> LDS stage j % 2, barrier, refill the registers
-  // with tile j + PF, compute tile j. Stage j % 2 was last read by tile
-  // j - 2, which every wave finished before the barrier of tile j - 1.
-  auto step = [&](int j, Staged &T) {
-    char *kt = lds[j & 1][0];
-    char *vt = lds[j & 1][1];
+  // registers -> LDS (16-bit values; FP8 codes widened with their row scale)
+  auto store_tile = [&](const Staged &T, char *kt, char *vt) {
     char *mine = cp_v ? vt : kt;
 #pragma unroll
     for (int u = 0; u < PPL; ++u) {
@@ -451,10 +460,19 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
         *reinterpret_cast<v4u32 *>(mine + cp_lds[u]) = T.d[u];
       }
     }
-    const uint32_t mask = T.blocks;
+  };
+
+  // Tile j: registers -> LDS stage j % 2, barrier, refill the registers
+  // with tile j + PF, compute tile j. Stage j % 2 was last read by tile
+  // j - 2, which every wave finished before the barrier of tile j - 1.
+  auto step = [&](int j, Staged &T) {
+    char *kt = lds[j & 1][0];
+    char *vt = lds[j & 1][1];
+    store_tile(T, kt, vt);
+    const uint32_t holes_t = T.holes;
     __syncthreads();
     if (j + PF < n_tiles) fetch(j + PF, T);
-    compute(kt, vt, j * PT, mask);
+    compute(kt, vt, j * PT, holes_t);
   };
 #if IKL_PREFILL_PREFETCH == 2
   Staged ta, tb;

@@ -6,7 +6,9 @@ Covered: the reference test's own geometry (fp32), the MFMA family over
 head_dim {32, 64, 96, 128}, MHA / GQA / MQA and a non-power-of-two group,
 block sizes 16 / 32 / 48, chunked prefill (chunks starting past 0), padding
 rows, positions past the chunk end poisoned with NaN, strided query/output
-views, the VALU family forced on the same inputs, and a long GQA chunk."""
+views, the VALU family forced on the same inputs, a long GQA chunk, and
+table entries outside the cache (their keys are dropped, as in the decode
+kernels)."""
 
 import numpy as np
 import pytest
@@ -160,3 +162,59 @@ def test_reference_validation_messages_on_gpu():
         paged_prefill_attention_hip(q, cache, [[0, 1]], [0], [9])
     with pytest.raises(ValueError, match="query and cache must have the same dtype"):
         paged_prefill_attention_hip(q.float(), cache, [[0]], [0], [8])
+
+
+def _expected_dropping_blocks(case, dropped, scale=None):
+    """The oracle's prefill attention with the keys of the logical blocks in
+    dropped[b] removed from every row of request b (no row loses all of its
+    keys here: block 0 stays)."""
+    from oracle import paged_oracle as po
+
+    oc = case.base.oracle_cache
+    q = case.query_f32
+    _, heads, _, dim = q.shape
+    sc = np.float32(scale if scale is not None else dim ** -0.5)
+    out = np.empty_like(q)
+    for b, (s, e) in enumerate(zip(case.starts, case.ends)):
+        k_raw, v_raw = oc.read(0, case.base.tables[b], e)
+        k = po.expand_kv(po.to_f32(k_raw, oc.dtype), heads).transpose(1, 0, 2)
+        v = po.expand_kv(po.to_f32(v_raw, oc.dtype), heads).transpose(1, 0, 2)
+        keep = np.array([pos // oc.block_size not in dropped[b] for pos in range(e)])
+        n = e - s
+        allow = po.causal_allow(s + np.arange(n), e) & keep[None]
+        scores = np.where(allow[None], np.matmul(q[b, :, :n], k.transpose(0, 2, 1)) * sc, -np.inf)
+        scores = (scores - scores.max(axis=-1, keepdims=True)).astype(np.float32)
+        probs = np.exp(scores)
+        probs /= probs.sum(axis=-1, keepdims=True)
+        out[b, :, :n] = np.matmul(probs, v)
+        out[b, :, n:] = v[:, :1, :]
+    return out
+
+
+@pytest.mark.parametrize("heads,kv,dim,bs,starts,ends,dropped,dtype,path", [
+    # a hole past the first 1024 keys (the kernel's table window moves there)
+    (16, 4, 128, 16, [0, 40], [300, 1500], [{1, 5}, {3, 70}], "bfloat16", None),
+    (8, 2, 64, 48, [0, 10], [200, 130], [{1}, {2}], "float16", None),
+    (8, 2, 64, 16, [0, 10], [200, 130], [{1, 2}, {4}], "float16", "scalar_grouped"),
+])
+def test_table_entries_outside_the_cache_are_dropped(heads, kv, dim, bs, starts, ends, dropped, dtype, path):
+    from inferkernellab_amd import PreparedPagedPrefill
+
+    case = make_prefill_case(starts=starts, ends=ends, num_heads=heads, num_kv_heads=kv, head_dim=dim,
+                             block_size=bs, dtype=dtype, seed=dim + bs + 3)
+    nb = case.base.oracle_cache.num_blocks
+    width = max(len(t) for t in case.base.tables)
+    rows = []
+    for b, table in enumerate(case.base.tables):
+        row = list(table) + [0] * (width - len(table))
+        for i, lb in enumerate(sorted(dropped[b])):
+            row[lb] = -1 if i % 2 == 0 else nb + 5  # negative and past-the-end ids
+        rows.append(row)
+    tables = torch.tensor(rows, dtype=torch.int32, device="cuda")
+    q = case.device_query()
+    prep = PreparedPagedPrefill(case.base.device_cache(), tables, starts, ends, num_heads=heads,
+                                query_width=q.shape[2], path=path)
+    got = prep(q, 0)
+    torch.cuda.synchronize()
+    assert prep.path == (path or "mfma_grouped")
+    assert _err(got, _expected_dropping_blocks(case, dropped)) < ATOL[dtype]
