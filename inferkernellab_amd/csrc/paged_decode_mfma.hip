@@ -47,8 +47,14 @@ constexpr int TILE = 16;  // tokens per tile
 #ifndef IKL_MFMA_PREFETCH
 #define IKL_MFMA_PREFETCH 1
 #endif
+// Register budget: at least MIN waves per SIMD, so VGPRs + AGPRs <= 512 / MIN.
+// The FP8 kernels with 16-head units ask for 2: they then keep their
+// accumulators in VGPRs, without the accumulator-register copies the
+// compiler otherwise places in every tile (81 -> 78 us on the FP8 GQA decode
+// workload). The others keep the compiler's choice (the 32-head kernels
+// would spill; the 16-bit 16-head one measured no better).
 #ifndef IKL_MFMA_MIN_WAVES
-#define IKL_MFMA_WAVES_ATTR
+#define IKL_MFMA_WAVES_ATTR __attribute__((amdgpu_waves_per_eu(KV8 && NG == 1 ? 2 : 1, 8)))
 #else
 #define IKL_MFMA_WAVES_ATTR __attribute__((amdgpu_waves_per_eu(IKL_MFMA_MIN_WAVES, 8)))
 #endif
