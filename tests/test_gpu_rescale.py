@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from oracle import paged_oracle as po
-from tests.helpers import ATOL, make_case, make_prefill_case, max_abs_err
+from tests.helpers import ATOL, assert_close_up_to_output_rounding, make_case, make_prefill_case, max_abs_err
 
 pytestmark = pytest.mark.gpu
 
@@ -23,17 +23,6 @@ def _to_storage(x: np.ndarray, dtype: str) -> np.ndarray:
     if dtype == "bfloat16":
         return po.f32_to_bf16_bits(x.astype(np.float32))
     return x.astype(po.storage_dtype(dtype))
-
-
-def _assert_close_up_to_output_rounding(out: torch.Tensor, expected: np.ndarray, dtype: str) -> None:
-    """|out - expected| <= ATOL + half an ulp of the output dtype at |expected|."""
-    got = out.float().cpu().numpy()
-    assert not np.isnan(got).any()
-    bits = {"bfloat16": 8, "float16": 11}[dtype]  # significand bits
-    _, e = np.frexp(np.abs(expected).astype(np.float64))
-    half_ulp = np.ldexp(1.0, e - bits - 1)
-    excess = np.abs(got - expected) - (ATOL[dtype] + half_ulp)
-    assert excess.max() <= 0, f"max excess {excess.max()}"
 
 
 def _grow_keys(case, lengths, dtype):
@@ -101,4 +90,4 @@ def test_prefill_rescale_with_growing_keys(dtype):
     got = prep(q, 0)
     torch.cuda.synchronize()
     assert prep.path == "mfma_grouped"
-    _assert_close_up_to_output_rounding(got, case.expected(), dtype)
+    assert_close_up_to_output_rounding(got, case.expected(), dtype)
