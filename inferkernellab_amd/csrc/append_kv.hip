@@ -34,7 +34,7 @@ template <int CHUNK>
 struct chunk_t;
 template <>
 struct chunk_t<16> {
-  using type = u32x4;
+  using type = v4u32;  // a vector type: loads and stores stay in registers
 };
 template <>
 struct chunk_t<4> {
@@ -49,16 +49,28 @@ template <typename IdxT, int CHUNK>
 __global__ __launch_bounds__(256) void append_kv_kernel(AppendParams p) {
   using C = typename chunk_t<CHUNK>::type;
   const int64_t t = blockIdx.x;
-  const int64_t slot = (int64_t)reinterpret_cast<const IdxT *>(p.slots)[t];
-  if (slot < 0 || slot >= p.num_slots) return;
-  const int64_t blk = slot / p.block_size;
-  const int64_t off = slot - blk * p.block_size;
   const int total = p.num_kv_heads * p.chunks_per_head;
   const char *ksrc = p.key + t * p.key_st;
   const char *vsrc = p.value + t * p.value_st;
+  // The first chunk's K/V loads do not depend on the slot: they go out with
+  // the slot load, so the copy costs one memory round trip before its stores.
+  const bool has0 = (int)threadIdx.x < total;
+  const int i0 = has0 ? (int)threadIdx.x : total - 1;  // in bounds either way; unused when !has0
+  const int h0 = i0 / p.chunks_per_head, c0 = i0 - h0 * p.chunks_per_head;
+  const int64_t slot = (int64_t)reinterpret_cast<const IdxT *>(p.slots)[t];
+  const C kv0 = *reinterpret_cast<const C *>(ksrc + h0 * p.key_sh + c0 * CHUNK);
+  const C vv0 = *reinterpret_cast<const C *>(vsrc + h0 * p.value_sh + c0 * CHUNK);
+  asm volatile("" ::"v"(kv0), "v"(vv0));  // all three loads issued before the slot test
+  if (slot < 0 || slot >= p.num_slots) return;
+  const int64_t blk = slot / p.block_size;
+  const int64_t off = slot - blk * p.block_size;
   char *kdst = p.kc + blk * p.kc_sb + off * p.kc_st;
   char *vdst = p.vc + blk * p.vc_sb + off * p.vc_st;
-  for (int i = threadIdx.x; i < total; i += blockDim.x) {
+  if (has0) {
+    *reinterpret_cast<C *>(kdst + h0 * p.kc_sh + c0 * CHUNK) = kv0;
+    *reinterpret_cast<C *>(vdst + h0 * p.vc_sh + c0 * CHUNK) = vv0;
+  }
+  for (int i = (int)threadIdx.x + (int)blockDim.x; i < total; i += blockDim.x) {
     const int h = i / p.chunks_per_head;
     const int c = i - h * p.chunks_per_head;
     const C kv = *reinterpret_cast<const C *>(ksrc + h * p.key_sh + c * CHUNK);
