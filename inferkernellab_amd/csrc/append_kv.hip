@@ -140,13 +140,17 @@ __global__ __launch_bounds__(64) void append_kv_fp8_kernel(Fp8AppendParams p) {
   const int which = blockIdx.x & 1;  // 0: key, 1: value
   const int h = (int)(blockIdx.x >> 1);
   const int64_t t = blockIdx.y;
+  const bool on = 4 * lane < p.head_dim;
+  // The row load does not depend on the slot: both go out together (lanes
+  // past the row read its first chunk, which exists, and drop it).
+  float x[4];
+  load4<Tag>(p.src[which] + t * p.src_st[which] + h * p.src_sh[which] + (on ? 4 * lane * EB : 0), x);
   const int64_t slot = (int64_t)reinterpret_cast<const IdxT *>(p.slots)[t];
+  asm volatile("" ::"v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]));
   if (slot < 0 || slot >= p.num_slots) return;
+  if (!on) x[0] = x[1] = x[2] = x[3] = 0.f;
   const int64_t blk = slot / p.block_size;
   const int64_t off = slot - blk * p.block_size;
-  const bool on = 4 * lane < p.head_dim;
-  float x[4] = {0.f, 0.f, 0.f, 0.f};
-  if (on) load4<Tag>(p.src[which] + t * p.src_st[which] + h * p.src_sh[which] + 4 * lane * EB, x);
   const float amax = wave_max(fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))));
   const float scale = e4m3_row_scale(amax);
   float y[4];
