@@ -122,13 +122,18 @@ __device__ inline int64_t clamped_ctx(const AttnParams &p, int64_t b) {
   return c < p.cap_tokens ? c : p.cap_tokens;
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave.
+// Inclusive prefix sum over the 64 lanes of a wave, in DPP moves (no LDS
+// round trips): a Hillis-Steele scan inside each 16-lane row (row_shr 1, 2,
+// 4, 8; lanes without a source add 0), then lane 15 of rows 0 and 2 into
+// rows 1 and 3 (row_bcast:15) and lane 31 into rows 2 and 3 (row_bcast:31).
 __device__ inline int wave_incl_scan(int x, int lane) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int y = __shfl_up(x, d, 64);
-    if (lane >= d) x += y;
-  }
+  (void)lane;
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15, rows 1 and 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31, rows 2 and 3
   return x;
 }
 
@@ -150,7 +155,7 @@ __device__ inline int64_t request_tiles(const AttnParams &p, int64_t b, int lane
       *own = __shfl(n, l, 64);
       *before = base + __shfl(incl, l, 64) - *own;
     }
-    base += __shfl(incl, 63, 64);
+    base += __builtin_amdgcn_readlane(incl, 63);
   }
   total = base;
   return total;

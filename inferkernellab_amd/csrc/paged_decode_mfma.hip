@@ -528,18 +528,33 @@ __global__ __launch_bounds__(64) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_stre
   const int lane = threadIdx.x;
   const int64_t U = p.units;
 
-  // total tiles, then the request holding this wave's first tile
-  int64_t before0;
-  int own0;
-  const int64_t total = request_tiles(p, 0, lane, &before0, &own0);
+  // total tiles, then the request holding this wave's first tile (a batch
+  // of up to 64 requests takes one scan for both)
+  int64_t total, b = -1, pb = 0;
+  int nb = 0, n1 = 0, incl1 = 0;
+  if (p.batch <= 64) {
+    n1 = lane < p.batch ? (int)((clamped_ctx(p, lane) + 15) >> 4) : 0;
+    incl1 = wave_incl_scan(n1, lane);
+    total = __builtin_amdgcn_readlane(incl1, 63);
+  } else {
+    int64_t before0;
+    int own0;
+    total = request_tiles(p, 0, lane, &before0, &own0);
+  }
   const int64_t T = U * total;
   const int64_t W = (int64_t)p.sk_waves < T ? (int64_t)p.sk_waves : T;
   const int64_t w = blockIdx.x;
   if (w >= W) return;
   const int64_t g0 = w * T / W, g1 = (w + 1) * T / W;
 
-  int64_t b = -1, pb = 0, base = 0;
-  int nb = 0;
+  if (p.batch <= 64) {
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < p.batch && U * incl1 > g0);
+    const int l = __builtin_ctzll(hit);  // g0 < T: some request's tiles end past it
+    b = l;
+    nb = __shfl(n1, l, 64);
+    pb = __shfl(incl1, l, 64) - nb;
+  }
+  int64_t base = 0;
   for (int64_t c0 = 0; c0 < p.batch && b < 0; c0 += 64) {
     const int64_t r = c0 + lane;
     const int n = r < p.batch ? (int)((clamped_ctx(p, r) + 15) >> 4) : 0;
