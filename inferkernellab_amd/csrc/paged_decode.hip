@@ -312,15 +312,16 @@ __global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParam
 // Combines the split partials of one (request, head):
 //   out = sum_p 2^(lse_p - M) o_p / sum_p 2^(lse_p - M),  M = max_p lse_p.
 // Lanes split into GROUPS groups of D/4 lanes; group j takes partitions
-// j, j+GROUPS, ... with 16-byte loads, so the loads of all partitions are in
-// flight together; the groups then combine through LDS.
+// j, j+GROUPS, ... with 16-byte loads (the log-sum-exp and the row of a
+// partition are loaded together, several partitions in flight), keeping its
+// own running maximum; the groups then combine through LDS.
 template <typename Tag, int D>
 __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(const AttnParams p) {
   constexpr int EB = elem<Tag>::bytes;
   constexpr int CH = D / 4;           // float4 chunks per row
   constexpr int GROUPS = 64 / CH;     // partition groups
   __shared__ float4 part_sum[GROUPS][CH];
-  __shared__ float part_z[GROUPS];
+  __shared__ float part_z[GROUPS], part_m[GROUPS];
   const int lane = threadIdx.x;
   const int64_t hq = blockIdx.x;
   const int64_t b = blockIdx.y;
@@ -351,40 +352,49 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(const AttnParam
     prow = b * p.num_parts * p.num_heads + hq;
     pstride = p.num_heads;
   }
-  float mx = -INFINITY;
-  for (int i = lane; i < np; i += 64) mx = fmaxf(mx, p.part_lse[prow + i * pstride]);
-#pragma unroll
-  for (int mask = 1; mask < 64; mask <<= 1) mx = fmaxf(mx, shfl_xor_f(mx, mask));
+  // One pass over the partials: each group keeps its own running maximum
+  // (online softmax over its partitions), and the groups meet in LDS.
   const int grp = lane / CH;
   const int ch = lane % CH;
-  float4 a = {0.f, 0.f, 0.f, 0.f};
-  float z = 0.f;
   if (grp < GROUPS) {
+    float4 a = {0.f, 0.f, 0.f, 0.f};
+    float z = 0.f, m = -INFINITY;
 #pragma unroll 4
     for (int i = grp; i < np; i += GROUPS) {
-      const float w = fast_exp2(p.part_lse[prow + i * pstride] - mx);
+      const float l = p.part_lse[prow + i * pstride];
       const float4 o = reinterpret_cast<const float4 *>(p.part_o + (prow + i * pstride) * D)[ch];
-      z += w;
-      a.x = fmaf(w, o.x, a.x);
-      a.y = fmaf(w, o.y, a.y);
-      a.z = fmaf(w, o.z, a.z);
-      a.w = fmaf(w, o.w, a.w);
+      const float mn = fmaxf(m, l);
+      const float c = mn == -INFINITY ? 1.f : fast_exp2(m - mn);  // rescale of what is summed so far
+      const float w = mn == -INFINITY ? 0.f : fast_exp2(l - mn);  // empty partitions (-inf) weigh 0
+      z = fmaf(z, c, w);
+      a.x = fmaf(w, o.x, a.x * c);
+      a.y = fmaf(w, o.y, a.y * c);
+      a.z = fmaf(w, o.z, a.z * c);
+      a.w = fmaf(w, o.w, a.w * c);
+      m = mn;
     }
     part_sum[grp][ch] = a;
-    if (ch == 0) part_z[grp] = z;
+    if (ch == 0) {
+      part_z[grp] = z;
+      part_m[grp] = m;
+    }
   }
   __syncthreads();
   if (lane >= CH) return;
-  float4 t = part_sum[0][lane];
-  float zt = part_z[0];
+  float mx = part_m[0];
 #pragma unroll
-  for (int j = 1; j < GROUPS; ++j) {
+  for (int j = 1; j < GROUPS; ++j) mx = fmaxf(mx, part_m[j]);
+  float4 t = {0.f, 0.f, 0.f, 0.f};
+  float zt = 0.f;
+#pragma unroll
+  for (int j = 0; j < GROUPS; ++j) {
+    const float f = part_m[j] == -INFINITY ? 0.f : fast_exp2(part_m[j] - mx);
     const float4 u = part_sum[j][lane];
-    t.x += u.x;
-    t.y += u.y;
-    t.z += u.z;
-    t.w += u.w;
-    zt += part_z[j];
+    t.x = fmaf(f, u.x, t.x);
+    t.y = fmaf(f, u.y, t.y);
+    t.z = fmaf(f, u.z, t.z);
+    t.w = fmaf(f, u.w, t.w);
+    zt = fmaf(f, part_z[j], zt);
   }
   const float inv = 1.f / zt;
   const float v[4] = {t.x * inv, t.y * inv, t.z * inv, t.w * inv};
