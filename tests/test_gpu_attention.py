@@ -192,6 +192,33 @@ def test_balanced_split_more_than_64_requests(dtype):
     _check(case, "paged_decode_attention_hip", label="sk-70")
 
 
+@pytest.mark.parametrize("batch", [15, 16, 17, 31, 33, 48, 63, 65])
+def test_balanced_split_request_scan_boundaries(batch):
+    """Batches around the in-kernel scan's 16-lane rows and its 64-request
+    chunk (one scan for up to 64 requests, the chunked walk beyond). Two
+    requests are emptied on the device (validate_inputs=False), so some
+    requests own no tiles: their rows are NaN, the others match the oracle."""
+    from inferkernellab_amd import ops
+
+    gen = np.random.default_rng(400 + batch)
+    lengths = [int(x) for x in gen.integers(1, 600, size=batch)]
+    case = make_case(batch=batch, num_heads=8, num_kv_heads=2, head_dim=64, block_size=16,
+                     lengths=lengths, dtype="bfloat16", seed=401 + batch)
+    empty = [batch // 2, batch - 1]
+    print(f"scan boundary case batch={batch} empty={empty} lens={lengths[:8]}", flush=True)
+    lens = case.device_lengths()
+    for b in empty:
+        lens[b] = 0
+    out = ops.paged_decode_attention_hip(case.device_query(), case.device_cache(), case.device_tables(), lens,
+                                         validate_inputs=False)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    expected = case.expected()
+    full = [b for b in range(batch) if b not in empty]
+    assert np.isnan(got[empty]).all(), "an empty context gives NaN rows (softmax over nothing)"
+    assert np.abs(got[full] - expected[full]).max() <= ATOL["bfloat16"]
+
+
 def test_balanced_split_one_unit_across_many_waves():
     """One MQA request of 20000 tokens: 1250 tiles, one unit split over ~1250 waves."""
     case = make_case(batch=1, num_heads=8, num_kv_heads=1, head_dim=128, block_size=32,
