@@ -36,8 +36,14 @@ namespace {
 
 constexpr int TILE = 16;  // tokens per tile
 
-// Tuning knobs: tiles prefetched ahead of the one computing (1 or 2), and an
-// optional minimum-occupancy request to the register allocator.
+// Build-time knobs; the defaults are the measured best:
+//   IKL_MFMA_SPLIT_P     bf16 P enters the PV product with its rounding
+//                        residual in a second MFMA (below);
+//   IKL_MFMA_HEAD_MAJOR  fixed partitions: the kv heads of one partition
+//                        are dispatched together;
+//   IKL_MFMA_PREFETCH    tiles in flight ahead of the one computing (1 or 2);
+//   IKL_MFMA_MIN_WAVES   one minimum waves-per-SIMD request for every kernel
+//                        (unset: the per-kernel choice below).
 #ifndef IKL_MFMA_SPLIT_P
 #define IKL_MFMA_SPLIT_P 1
 #endif
