@@ -73,10 +73,14 @@ def test_partition_planning_for_the_gqa_decode_shape():
     a = _args(partition_size=-1, max_context_len=8192)
     assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 0
     assert lib.ikl_paged_attention_workspace_size(ctypes.byref(a)) == 0
-    # automatic on the scalar family: short contexts with few workgroups
-    # shrink the fixed partition
+    # automatic on the scalar family: 512 tokens, halved (down to 128) while
+    # there are fewer than 1024 workgroups (one wave per SIMD of 256 CUs)
     a = _args(partition_size=0, max_context_len=512, batch=16, num_kv_heads=32, dtype=_lib.IKL_F32)
-    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 128
+    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 256  # 512 units x 2 partitions
+    a = _args(partition_size=0, max_context_len=512, batch=4, num_kv_heads=32, dtype=_lib.IKL_F32)
+    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 128  # the floor
+    a = _args(partition_size=0, max_context_len=8192, batch=16, num_kv_heads=32, dtype=_lib.IKL_F32)
+    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 512  # 512 x 16 >= 1024 already
 
 
 def test_balanced_split_planning_on_the_mfma_family():
