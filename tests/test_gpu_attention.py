@@ -49,9 +49,20 @@ def test_grouped_reference_shape(num_kv_heads, dtype):
 
 @pytest.mark.parametrize("query_group_size", [1, 2, 4, 8])
 def test_grouped_query_group_sizes(query_group_size):
+    """The grouped wrapper (whose matrix-core path shares each tile among all
+    6 heads of a KV head), then the C ABI with units of exactly
+    min(query_group_size, 6) heads on the matrix cores."""
+    from inferkernellab_amd import ops
+
     case = make_case(batch=3, num_heads=12, num_kv_heads=2, head_dim=64, block_size=16,
                      lengths=[100, 7, 333], dtype="bfloat16", seed=20)
     _check(case, "paged_decode_attention_hip_grouped", label="qgs", query_group_size=query_group_size)
+    attn = ops.PreparedPagedAttention(case.device_query(), case.device_cache(), case.device_tables(),
+                                      case.device_lengths(), query_group_size=query_group_size)
+    out = attn()
+    torch.cuda.synchronize()
+    assert attn.path == "mfma_grouped"
+    assert max_abs_err(out, case.expected()) <= ATOL["bfloat16"]
 
 
 @pytest.mark.parametrize("head_dim", [16, 32, 64, 96, 128])

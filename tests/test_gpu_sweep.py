@@ -3,6 +3,8 @@ oracle. Each case draws a dtype, head_dim, block size, KV heads and heads
 per KV head, a query group size, ragged lengths (with 1 and the block edges
 over-represented), the split mode, the block layout and, where the MFMA
 family runs, the FP8 cache, then checks the kernels through the C ABI.
+Even decode cases call the reference's grouped signature, odd ones the C
+ABI with the drawn query group size as the exact unit size.
 Tolerance: max-abs 2e-3 fp16 / 1e-2 bf16 / 1e-4 fp32 against the fp32
 oracle, plus half an ulp of the output at its magnitude (the rounding of
 the output itself). Every case prints its configuration before it runs."""
@@ -91,9 +93,14 @@ def test_decode_sweep(i):
         cache = _fp8_device_cache(case, cfg["head_major"], cfg["dtype"])
     else:
         cache = _device_cache(case, cfg["head_major"])
-    out = ops.paged_decode_attention_hip_grouped(query, cache, case.device_tables(), case.device_lengths(),
-                                                 query_group_size=cfg["query_group_size"],
-                                                 partition_size=cfg["partition"])
+    if i % 2 == 0:  # the reference's grouped signature
+        out = ops.paged_decode_attention_hip_grouped(query, cache, case.device_tables(), case.device_lengths(),
+                                                     query_group_size=cfg["query_group_size"],
+                                                     partition_size=cfg["partition"])
+    else:  # the C ABI's explicit group size (units of exactly that many heads)
+        out = ops.PreparedPagedAttention(query, cache, case.device_tables(), case.device_lengths(),
+                                         query_group_size=cfg["query_group_size"],
+                                         partition_size=cfg["partition"])()
     torch.cuda.synchronize()
     expected = po.paged_decode_attention(expected_q, case.oracle_cache, case.tables, case.lengths)
     assert_close_up_to_output_rounding(out, expected, cfg["dtype"])
