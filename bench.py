@@ -57,6 +57,13 @@ WORKLOADS = {
     "mqa32x1_hd128_bf16_b64_ctx1k-4k": (64, 32, 1, 128, torch.bfloat16, 1024, 4096, None, 0.5, None),
     # the GQA decode shape over the FP8 (E4M3, per-row scale) cache format
     "gqa32x8_hd128_fp8kv_b32_ctx4k-8k": (32, 32, 8, 128, torch.bfloat16, 4096, 8192, 20000, 1.0, None, "fp8"),
+    # the shapes the reference publishes its Triton kernel's A100 timings on (head_dim 64, block 16,
+    # uniform contexts; docs/benchmark_report.md:45-52)
+    "gqa32x8_hd64_fp16_b4_ctx512": (4, 32, 8, 64, torch.float16, 512, 512, None, 1.0, None),
+    "gqa32x8_hd64_fp16_b16_ctx2k": (16, 32, 8, 64, torch.float16, 2048, 2048, None, 1.0, None),
+    "gqa32x8_hd64_bf16_b16_ctx2k": (16, 32, 8, 64, torch.bfloat16, 2048, 2048, None, 1.0, None),
+    "mha32_hd64_fp16_b16_ctx2k": (16, 32, 32, 64, torch.float16, 2048, 2048, None, 1.0, None),
+    "mqa32x1_hd64_bf16_b16_ctx2k": (16, 32, 1, 64, torch.bfloat16, 2048, 2048, None, 1.0, None),
 }
 DEFAULT_WORKLOAD = "gqa32x8_hd128_bf16_b32_ctx4k-8k"
 
