@@ -131,7 +131,9 @@ typedef struct ikl_paged_attention_args {
    * of a KV head (capped by the kernel family), else 1..heads_per_kv. */
   int32_t query_group_size;
   /* Tokens per split-context partition: 0 = pick automatically, -1 = never
-   * split (one pass per request), else a positive multiple of 64. */
+   * split (one pass per request), -2 = the balanced split (MFMA family:
+   * equal runs of the batch's tiles per wave), else a positive multiple of
+   * 64. */
   int32_t partition_size;
   /* Host-known upper bound of context_lens (0 = table_width*block_size);
    * only sizes the grid, never read from device memory. */

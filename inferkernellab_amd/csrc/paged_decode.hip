@@ -519,21 +519,32 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
   pl.units = (int64_t)a->num_kv_heads * pl.groups_per_kv;
   const int64_t units = a->batch * pl.units;
 
-  // Automatic split on the MFMA family: the balanced split (one run of
-  // ~T/W tiles per resident wave). Its in-kernel sums need a 64-request
-  // chunk of tile counts to fit in 32 bits (cap < 2^29 tokens) and
-  // (T + 1) * W to fit in 63 bits.
-  if (a->partition_size == 0 && pl.path == IKL_PATH_MFMA_GROUPED && cap < (int64_t(1) << 29)) {
-    const int64_t t_max = units * ((maxctx + 15) / 16);
-// At least this many tiles per wave at the longest context: short or small
-// batches then run fewer, longer waves instead of one tile each (ragged
-// contexts give some waves fewer). Measured op times, 1 -> 4: Llama 16/4
-// hd128 B16 x 544 tokens 17.6 -> 16.6 us, GQA 32/8 hd128 B8 x 1024 19.2 ->
-// 17.5 us, MQA 32/1 hd64 B16 x 2048 24.9 -> 16.5 us; large batches keep
-// the resident capacity.
+  // Balanced split waves: at least IKL_SK_MIN_TILES tiles each at the
+  // longest context (a small batch runs fewer, longer waves, not one tile
+  // each; e.g. MQA 32/1 hd64 B16 x 2048: 24.9 -> 16.5 us going from 1 to 4),
+  // capped by the resident capacity.
 #ifndef IKL_SK_MIN_TILES
 #define IKL_SK_MIN_TILES 4
 #endif
+  // The balanced split on the MFMA family (one run of ~T/W tiles per
+  // resident wave): asked for with partition_size = -2, and picked
+  // automatically above SK_MIN_BATCH_TILES tiles at the longest context.
+  // Below that, fixed partitions (4-wave workgroups merging in LDS, one
+  // partial per partition) measured faster on the whole operation (split
+  // kernel + reduce, MALL flushed): MQA 32/1 hd128 B64 x U[1024, 4096]
+  // 35.8 -> 31.5 us, GQA 32/8 hd128 B64 x 512 35.9 -> 30.2 us, B32 x 2048
+  // 58.1 -> 56.3 us, the Llama decode shape (16/4, B16 x 544) 16.7 -> 15.0
+  // us; above it the balanced split wins (B32 x U[4096, 8192] 145 vs 168
+  // us, B16 x U[4096, 8192] 77 vs 87 us). Its in-kernel sums need a
+  // 64-request chunk of tile counts to fit in 32 bits (cap < 2^29 tokens)
+  // and (T + 1) * W to fit in 63 bits.
+  constexpr int64_t SK_MIN_BATCH_TILES = 32768;
+  if (a->partition_size == -2 && pl.path != IKL_PATH_MFMA_GROUPED)
+    return fail(IKL_EUNSUPPORTED, "partition_size -2 (the balanced split) needs the MFMA kernel family");
+  const int64_t t_max = units * ((maxctx + 15) / 16);
+  const bool want_balanced =
+      a->partition_size == -2 || (a->partition_size == 0 && pl.path == IKL_PATH_MFMA_GROUPED && t_max > SK_MIN_BATCH_TILES);
+  if (want_balanced && cap < (int64_t(1) << 29)) {
     const int64_t w = std::min<int64_t>(mfma_streamk_capacity(a->dtype, a->head_dim, pl.group_size, pl.kv_fp8),
                                         std::max<int64_t>((t_max + IKL_SK_MIN_TILES - 1) / IKL_SK_MIN_TILES, 1));
     if ((double)(t_max + 1) * (double)w < 4.0e18) {
@@ -554,6 +565,10 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
     if (a->partition_size % 64 != 0)
       return fail(IKL_EINVAL, "partition_size must be a positive multiple of 64");
     P = a->partition_size;
+  } else if (pl.path == IKL_PATH_MFMA_GROUPED) {
+    // 512 tokens, halved to 256 while fewer than 256 workgroups
+    P = 512;
+    if (units * ((maxctx + P - 1) / P) < 256) P = 256;
   } else {
     P = 512;
     // one wave per SIMD of the 256 CUs: on the MHA shapes measured, longer

@@ -338,7 +338,8 @@ def paged_decode_attention_hip(
     All query heads of a KV head share each K/V tile in one workgroup (the
     kernel family is picked by :func:`paged_decode_grouped_path`). Extra
     keyword-only knobs: ``partition_size`` (tokens per split-context
-    partition; ``-1`` never splits, ``None`` picks automatically),
+    partition; ``-1`` never splits, ``-2`` asks for the matrix-core
+    family's balanced split, ``None`` picks automatically),
     ``max_context_len`` (a host-known bound of ``context_lens`` used to size
     the split grid) and ``events`` (up to three raw hipEvent_t handles
     recorded before the attention kernel, after it and after the split

@@ -100,6 +100,34 @@ def test_balanced_split_planning_on_the_mfma_family():
         assert ws == -(-(rows * 128 * 4) // 256) * 256 + rows * 4
 
 
+def test_split_choice_by_batch_size_on_the_mfma_family():
+    """Automatic on the MFMA family: the balanced split above 32768 tiles at
+    the longest context, fixed partitions below it (512 tokens, 256 while
+    fewer than 256 workgroups); -2 asks for the balanced split at any size
+    and only on the MFMA family."""
+    lib = _lib.load()
+    # B32 x 8 kv heads x 8192 tokens: 131072 tiles -> balanced (partition = a wave's run)
+    a = _args(partition_size=0, max_context_len=8192)
+    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) not in (256, 512, 0)
+    # B32 x 8 x 1024: 16384 tiles -> fixed 512-token partitions (512 workgroups)
+    a = _args(partition_size=0, max_context_len=1024)
+    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 512
+    # B2 x 8 x 1024: 32 units x 2 partitions < 256 workgroups -> 256-token partitions
+    a = _args(partition_size=0, max_context_len=1024, batch=2)
+    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 256
+    # B32 x 512: one 512-token partition covers the context -> no split
+    a = _args(partition_size=0, max_context_len=512)
+    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 0
+    # -2: the balanced split on a small batch too
+    a = _args(partition_size=-2, max_context_len=1024, batch=2)
+    part = lib.ikl_paged_attention_partition_size(ctypes.byref(a))
+    assert part > 0 and part % 16 == 0 and part not in (256, 512)
+    # -2 on the scalar family is refused
+    a = _args(partition_size=-2, max_context_len=1024, dtype=_lib.IKL_F32)
+    assert lib.ikl_paged_attention_workspace_size(ctypes.byref(a)) == _lib.IKL_EUNSUPPORTED
+    assert "balanced split" in _lib.last_error()
+
+
 def test_invalid_arguments_report_errors():
     lib = _lib.load()
     a = _args(num_heads=30)

@@ -189,8 +189,9 @@ def test_repeat_runs_are_bit_identical():
 
 
 # ---------------------------------------------------------------- balanced split
-# partition_size=None on the MFMA family runs the balanced split: the batch's
-# tiles are cut into one equal run per resident wave and merged per unit.
+# partition_size=-2 runs the MFMA family's balanced split (None picks it for
+# batches above 32768 tiles): the batch's tiles are cut into one equal run
+# per wave and merged per unit.
 
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 def test_balanced_split_more_than_64_requests(dtype):
@@ -200,7 +201,7 @@ def test_balanced_split_more_than_64_requests(dtype):
     lengths[0], lengths[63], lengths[64], lengths[69] = 1, 16, 17, 1000
     case = make_case(batch=70, num_heads=16, num_kv_heads=4, head_dim=128, block_size=16,
                      lengths=lengths, dtype=dtype, seed=41)
-    _check(case, "paged_decode_attention_hip", label="sk-70")
+    _check(case, "paged_decode_attention_hip", label="sk-70", partition_size=-2)
 
 
 @pytest.mark.parametrize("batch", [15, 16, 17, 31, 33, 48, 63, 65])
@@ -221,7 +222,7 @@ def test_balanced_split_request_scan_boundaries(batch):
     for b in empty:
         lens[b] = 0
     out = ops.paged_decode_attention_hip(case.device_query(), case.device_cache(), case.device_tables(), lens,
-                                         validate_inputs=False)
+                                         validate_inputs=False, partition_size=-2)
     torch.cuda.synchronize()
     got = out.float().cpu().numpy()
     expected = case.expected()
@@ -234,17 +235,17 @@ def test_balanced_split_one_unit_across_many_waves():
     """One MQA request of 20000 tokens: 1250 tiles, one unit split over ~1250 waves."""
     case = make_case(batch=1, num_heads=8, num_kv_heads=1, head_dim=128, block_size=32,
                      lengths=[20000], dtype="bfloat16", seed=42)
-    _check(case, "paged_decode_attention_hip", label="sk-long")
+    _check(case, "paged_decode_attention_hip", label="sk-long", partition_size=-2)
 
 
 @pytest.mark.parametrize("lengths", [[1], [1, 1, 1], [15, 16, 17, 33]])
 def test_balanced_split_fewer_tiles_than_waves(lengths):
     case = make_case(batch=len(lengths), num_heads=8, num_kv_heads=2, head_dim=64, block_size=16,
                      lengths=lengths, dtype="float16", seed=43)
-    _check(case, "paged_decode_attention_hip", label="sk-tiny")
+    _check(case, "paged_decode_attention_hip", label="sk-tiny", partition_size=-2)
 
 
-@pytest.mark.parametrize("partition_size", [None, 256])
+@pytest.mark.parametrize("partition_size", [None, -2, 256])
 def test_empty_contexts_give_nan_rows_and_leave_others_exact(partition_size):
     """validate_inputs=False with zero-length requests: their rows are NaN
     (0/0, as the reference's softmax over nothing) in both split modes; the
@@ -265,7 +266,7 @@ def test_empty_contexts_give_nan_rows_and_leave_others_exact(partition_size):
         assert max_abs_err(out[b:b + 1], expected[b:b + 1]) <= ATOL["bfloat16"]
 
 
-@pytest.mark.parametrize("partition_size", [None, 128])
+@pytest.mark.parametrize("partition_size", [None, -2, 128])
 def test_context_past_table_capacity_is_masked(partition_size):
     """validate_inputs=False, context_lens beyond the table: positions with no
     table entry are masked, so the result is attention over the mapped part."""
@@ -295,7 +296,7 @@ def test_balanced_and_fixed_partitions_agree():
                      lengths=[4096, 17, 8192, 5000, 1, 6000, 333, 7777], dtype="bfloat16", seed=46)
     cache = case.device_cache()
     args = (case.device_query(), cache, case.device_tables(), case.device_lengths())
-    a = ops.paged_decode_attention_hip(*args)
+    a = ops.paged_decode_attention_hip(*args, partition_size=-2)
     b = ops.paged_decode_attention_hip(*args, partition_size=512)
     torch.cuda.synchronize()
     expected = case.expected()
@@ -387,7 +388,11 @@ def test_autotune_reporters_describe_the_last_launch():
     ops.paged_decode_attention_hip(case.device_query(), case.device_cache(), case.device_tables(),
                                    case.device_lengths())
     cfg = ops.paged_decode_grouped_dot_autotune_config()
-    assert cfg == {"block_n": 16, "num_warps": 1, "num_stages": 2}
+    assert cfg == {"block_n": 16, "num_warps": 4, "num_stages": 2}  # a small batch: fixed partitions
+    ops.paged_decode_attention_hip(case.device_query(), case.device_cache(), case.device_tables(),
+                                   case.device_lengths(), partition_size=-2)
+    cfg = ops.paged_decode_grouped_dot_autotune_config()
+    assert cfg == {"block_n": 16, "num_warps": 1, "num_stages": 2}  # the balanced split: one-wave groups
     case32 = make_case(batch=2, num_heads=8, num_kv_heads=8, head_dim=64, block_size=16,
                        lengths=[30, 40], dtype="float32", seed=51)
     ops.paged_decode_attention_hip(case32.device_query(), case32.device_cache(), case32.device_tables(),
@@ -406,7 +411,7 @@ def test_prepared_balanced_split_repeats_bit_identically(lengths, heads, kv):
     case = make_case(batch=len(lengths), num_heads=heads, num_kv_heads=kv, head_dim=128, block_size=16,
                      lengths=lengths, dtype="bfloat16", seed=47)
     attn = ops.PreparedPagedAttention(case.device_query(), case.device_cache(), case.device_tables(),
-                                      case.device_lengths(), max_context_len=max(lengths))
+                                      case.device_lengths(), max_context_len=max(lengths), partition_size=-2)
     assert attn.balanced_split
     first = attn().clone()
     for _ in range(4):

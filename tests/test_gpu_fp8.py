@@ -101,7 +101,7 @@ CASES = [
 
 @pytest.mark.parametrize("act", ["bfloat16", "float16"])
 @pytest.mark.parametrize("heads,kv,dim,bs,lengths", CASES)
-@pytest.mark.parametrize("partition", [None, 256, -1])
+@pytest.mark.parametrize("partition", [None, -2, 256, -1])
 def test_fp8_decode_attention_matches_oracle(act, heads, kv, dim, bs, lengths, partition):
     from inferkernellab_amd import ops
 

@@ -12,7 +12,7 @@ from tests.helpers import ATOL, make_case, max_abs_err
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("partition_size", [None, 256])
+@pytest.mark.parametrize("partition_size", [None, -2, 256])
 def test_captured_step_replays_match_eager(partition_size):
     from inferkernellab_amd import ops
 

@@ -36,7 +36,7 @@ def _grow_keys(case, lengths, dtype):
         oc.k[0, blk, off] = _to_storage(k, dtype)
 
 
-@pytest.mark.parametrize("partition", [None, 256])
+@pytest.mark.parametrize("partition", [None, -2, 256])
 @pytest.mark.parametrize("heads,kv,dtype", [(32, 8, "bfloat16"), (32, 1, "bfloat16"), (16, 4, "float16")])
 def test_decode_rescale_with_growing_keys(heads, kv, dtype, partition):
     from inferkernellab_amd import ops

@@ -36,8 +36,12 @@ def _decode_config(i: int) -> dict:
     batch = rng.randint(1, 6)
     lengths = [rng.choice([1, block_size, block_size + 1, rng.randint(1, 700), rng.randint(700, 4000)])
                for _ in range(batch)]
+    partition = rng.choice([None, -2, 256, -1, 64 * rng.randint(1, 8)])
+    mfma = fp8 or (dtype != "float32" and block_size % 16 == 0 and head_dim in (32, 64, 96, 128) and group > 1)
+    if partition == -2 and not mfma:  # the balanced split is the matrix-core family's
+        partition = None
     return dict(dtype=dtype, fp8=fp8, head_dim=head_dim, block_size=block_size, kv=kv, heads=kv * group,
-                lengths=lengths, partition=rng.choice([None, None, 256, -1, 64 * rng.randint(1, 8)]),
+                lengths=lengths, partition=partition,
                 query_group_size=rng.choice([1, 2, 4, 8]),  # the reference signature's values
                 head_major=(not fp8 and dtype != "float32" and rng.random() < 0.3) or (fp8 and rng.random() < 0.7),
                 seed=i)
