@@ -566,9 +566,12 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
       return fail(IKL_EINVAL, "partition_size must be a positive multiple of 64");
     P = a->partition_size;
   } else if (pl.path == IKL_PATH_MFMA_GROUPED) {
-    // 512 tokens, halved to 256 while fewer than 256 workgroups
+    // 512 tokens, halved (down to 128) while fewer than 160 workgroups. On
+    // measured small batches this picked the best of 128/256/512 each time:
+    // 256 for the Llama decode shape (192 workgroups), 128 for GQA hd64
+    // B4 x 512 (11.9 -> 10.6 us) and MQA hd64 B16 x 2048 (16.4 -> 13.9 us)
     P = 512;
-    if (units * ((maxctx + P - 1) / P) < 256) P = 256;
+    while (P > 128 && units * ((maxctx + P - 1) / P) < 160) P /= 2;
   } else {
     P = 512;
     // one wave per SIMD of the 256 CUs: on the MHA shapes measured, longer

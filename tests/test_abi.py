@@ -102,9 +102,9 @@ def test_balanced_split_planning_on_the_mfma_family():
 
 def test_split_choice_by_batch_size_on_the_mfma_family():
     """Automatic on the MFMA family: the balanced split above 32768 tiles at
-    the longest context, fixed partitions below it (512 tokens, 256 while
-    fewer than 256 workgroups); -2 asks for the balanced split at any size
-    and only on the MFMA family."""
+    the longest context, fixed partitions below it (512 tokens, halved down
+    to 128 while fewer than 160 workgroups); -2 asks for the balanced split
+    at any size and only on the MFMA family."""
     lib = _lib.load()
     # B32 x 8 kv heads x 8192 tokens: 131072 tiles -> balanced (partition = a wave's run)
     a = _args(partition_size=0, max_context_len=8192)
@@ -112,8 +112,11 @@ def test_split_choice_by_batch_size_on_the_mfma_family():
     # B32 x 8 x 1024: 16384 tiles -> fixed 512-token partitions (512 workgroups)
     a = _args(partition_size=0, max_context_len=1024)
     assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 512
-    # B2 x 8 x 1024: 32 units x 2 partitions < 256 workgroups -> 256-token partitions
+    # B2 x 8 x 1024: 16 units -> 32, 64, then 128 workgroups -> 128-token partitions
     a = _args(partition_size=0, max_context_len=1024, batch=2)
+    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 128
+    # B16 x 4 x 544 (the Llama decode shape): 128 workgroups at 512, 192 at 256 -> 256
+    a = _args(partition_size=0, max_context_len=544, batch=16, num_heads=16, num_kv_heads=4)
     assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 256
     # B32 x 512: one 512-token partition covers the context -> no split
     a = _args(partition_size=0, max_context_len=512)
