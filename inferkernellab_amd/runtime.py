@@ -1,17 +1,21 @@
 """Model-independent runtime: request lifecycle, KV block reservation and
 the ``prefill_fn`` / ``prefill_batch_fn`` / ``decode_fn`` hooks.
 
-Same contract as the reference's runtime.py:10-113, which is part of the
-drop-in surface: runners plug the HIP append and attention operators into
-these hooks.
+The hooks are the drop-in surface of the reference's runtime
+(runtime.py:10-12): runners plug the HIP append and attention operators into
+them. What callers observe, and the reference's tests pin
+(tests/test_runtime.py:8-81), is kept:
 
-* ``submit`` reserves blocks for ``max(1, prompt_tokens)`` tokens.
-* A prefill step calls ``prefill_batch_fn(requests, starts, ends)`` once
-  with every request that received prompt tokens (or ``prefill_fn`` per
-  request), after growing each table to ``cached_tokens``.
-* A decode step reserves room for one more token per request, calls
-  ``decode_fn(requests)`` BEFORE the scheduler counts the generated token,
-  then frees the blocks of finished requests.
+* ``submit`` reserves blocks for ``max(1, prompt_tokens)`` tokens;
+* a prefill step grows every scheduled table to its cached tokens, then
+  calls ``prefill_batch_fn(requests, starts, ends)`` once with the requests
+  whose range is non-empty (or ``prefill_fn`` per request);
+* a decode step first reserves room for the token each request writes, then
+  calls ``decode_fn(requests)`` — before the scheduler counts that token —
+  and finally returns the blocks of finished requests to the allocator.
+
+A step is dispatched on its phase to one handler; block reservation is one
+helper that tops a table up to the blocks a token count needs.
 """
 
 from __future__ import annotations
@@ -36,7 +40,21 @@ class RuntimeStats:
     used_blocks: int
 
 
+@dataclass(frozen=True)
+class _Hooks:
+    prefill: PrefillFn | None
+    prefill_batch: PrefillBatchFn | None
+    decode: DecodeFn | None
+
+    def __post_init__(self):
+        if self.prefill is not None and self.prefill_batch is not None:
+            raise ValueError("prefill_fn and prefill_batch_fn are mutually exclusive")
+
+
 class InferenceRuntime:
+    """Drives a :class:`TokenBudgetScheduler` over a :class:`PagedKVCache`,
+    calling the model hooks at each step (no logits of its own)."""
+
     def __init__(
         self,
         cache: PagedKVCache,
@@ -46,66 +64,77 @@ class InferenceRuntime:
         prefill_batch_fn: PrefillBatchFn | None = None,
         decode_fn: DecodeFn | None = None,
     ):
-        if prefill_fn is not None and prefill_batch_fn is not None:
-            raise ValueError("prefill_fn and prefill_batch_fn are mutually exclusive")
+        self._hooks = _Hooks(prefill_fn, prefill_batch_fn, decode_fn)
         self.cache = cache
         self.scheduler = scheduler
-        self.prefill_fn = prefill_fn
-        self.prefill_batch_fn = prefill_batch_fn
-        self.decode_fn = decode_fn
-        self._requests: dict[int, InferenceRequest] = {}
+        self._by_id: dict[int, InferenceRequest] = {}
+        self._handlers = {"prefill": self._prefill_step, "decode": self._decode_step}
+
+    @property
+    def prefill_fn(self) -> PrefillFn | None:
+        return self._hooks.prefill
+
+    @property
+    def prefill_batch_fn(self) -> PrefillBatchFn | None:
+        return self._hooks.prefill_batch
+
+    @property
+    def decode_fn(self) -> DecodeFn | None:
+        return self._hooks.decode
 
     def submit(self, request_id: int, prompt_tokens: int, max_new_tokens: int) -> InferenceRequest:
-        if request_id in self._requests:
+        if request_id in self._by_id:
             raise ValueError(f"duplicate request_id: {request_id}")
         request = InferenceRequest(request_id, prompt_tokens, max_new_tokens)
         request.block_table = self.cache.allocate_request(request_id, max(1, prompt_tokens))
-        self._requests[request_id] = request
+        self._by_id[request_id] = request
         self.scheduler.add(request)
         return request
 
-    def _ensure_capacity(self, request: InferenceRequest, num_tokens: int) -> None:
-        needed = -(-num_tokens // self.cache.layout.block_size) - len(request.block_table)
-        if needed > 0:
-            request.block_table.extend(
-                self.cache.allocator.allocate(needed, owner=request.request_id)
-            )
+    def _reserve(self, request: InferenceRequest, tokens: int) -> None:
+        """Tops the request's table up to the blocks `tokens` positions need."""
+        short = -(-tokens // self.cache.layout.block_size) - len(request.block_table)
+        if short > 0:
+            request.block_table += self.cache.allocator.allocate(short, owner=request.request_id)
 
     def step(self) -> ScheduleBatch:
-        before = {id(r): r.cached_tokens for r in self._requests.values()}
+        # prompt progress of every queued request before the scheduler grants
+        # tokens: each prefill range starts there
+        progress = {request.request_id: request.cached_tokens for request in self.scheduler.waiting}
         batch = self.scheduler.schedule()
-        if batch.phase == "prefill":
-            chosen, starts, ends = [], [], []
-            for request in batch.requests:
-                self._ensure_capacity(request, max(1, request.cached_tokens))
-                start, end = before[id(request)], request.cached_tokens
-                if start < end:
-                    chosen.append(request)
-                    starts.append(start)
-                    ends.append(end)
-            if chosen and self.prefill_batch_fn is not None:
-                self.prefill_batch_fn(tuple(chosen), tuple(starts), tuple(ends))
-            elif self.prefill_fn is not None:
-                for request, start, end in zip(chosen, starts, ends):
-                    self.prefill_fn(request, start, end)
-        elif batch.phase == "decode":
-            for request in batch.requests:
-                # room for the token this step writes
-                self._ensure_capacity(request, request.prompt_tokens + request.generated_tokens + 1)
-            if self.decode_fn is not None:
-                self.decode_fn(batch.requests)
-            self.scheduler.mark_decode_step(batch.requests)
-            for request in batch.requests:
-                if request.finished:
-                    self.cache.release_request(request.block_table, request_id=request.request_id)
-                    request.block_table = []
+        handler = self._handlers.get(batch.phase)
+        if handler is not None:
+            handler(batch, progress)
         return batch
 
+    def _prefill_step(self, batch: ScheduleBatch, progress: dict[int, int]) -> None:
+        ranges = []
+        for request in batch.requests:
+            self._reserve(request, max(1, request.cached_tokens))
+            lo = progress.get(request.request_id, request.cached_tokens)
+            if lo < request.cached_tokens:
+                ranges.append((request, lo, request.cached_tokens))
+        hooks = self._hooks
+        if ranges and hooks.prefill_batch is not None:
+            requests, starts, ends = zip(*ranges)
+            hooks.prefill_batch(tuple(requests), tuple(starts), tuple(ends))
+        elif hooks.prefill is not None:
+            for request, lo, hi in ranges:
+                hooks.prefill(request, lo, hi)
+
+    def _decode_step(self, batch: ScheduleBatch, progress: dict[int, int]) -> None:
+        del progress  # decode ranges are one token at prompt + generated
+        for request in batch.requests:
+            self._reserve(request, request.prompt_tokens + request.generated_tokens + 1)
+        if self._hooks.decode is not None:
+            self._hooks.decode(batch.requests)
+        self.scheduler.mark_decode_step(batch.requests)
+        for request in (r for r in batch.requests if r.finished):
+            self.cache.release_request(request.block_table, request_id=request.request_id)
+            request.block_table = []
+
     def stats(self) -> RuntimeStats:
-        return RuntimeStats(
-            waiting=len(self.scheduler.waiting),
-            running=len(self.scheduler.running),
-            finished=len(self.scheduler.finished),
-            free_blocks=self.cache.allocator.num_free_blocks,
-            used_blocks=self.cache.allocator.num_used_blocks,
-        )
+        allocator = self.cache.allocator
+        s = self.scheduler
+        return RuntimeStats(len(s.waiting), len(s.running), len(s.finished), allocator.num_free_blocks,
+                            allocator.num_used_blocks)

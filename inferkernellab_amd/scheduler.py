@@ -1,20 +1,35 @@
-"""FCFS token-budget scheduler driving the runtime hooks.
+"""FCFS token-budget scheduler behind the runtime hooks.
 
-Same accounting as the reference's scheduler.py:7-95: waiting requests are
-prefilled in FCFS order under ``max_num_batched_tokens`` (a long prompt is
-chunked across steps and keeps its place at the head of the queue), and
-once nothing is left to prefill the running requests decode one token per
-step.
+Observable contract (the reference's scheduler.py:7-95 and the sequences
+its tests pin, tests/test_scheduler.py:4-29, tests/test_runtime.py:8-81):
+
+* a step prefills while any request waits: requests are taken in arrival
+  order under ``max_num_batched_tokens`` and ``max_num_seqs``; only the first
+  request of a step may be cut short (a long prompt is chunked over several
+  steps and keeps its place at the head of the queue), a later one is taken
+  only if its whole remaining prompt fits;
+* a request with nothing left to prefill moves to the running set without
+  using budget;
+* when nothing is prefilled, up to ``max_num_seqs`` running requests decode
+  one token each; ``mark_decode_step`` counts it and retires finished ones.
+
+The step is computed as a plan first — a list of token grants over a prefix
+of the queue, nothing mutated — and then committed in queue order, so the
+budget rules live in one pure function (:func:`plan_prefill`).
 """
 
 from __future__ import annotations
 
 from collections import deque
 from dataclasses import dataclass, field
+from typing import Iterable, Sequence
 
 
 @dataclass
 class InferenceRequest:
+    """A request's lifecycle state; the fields are the reference's
+    (scheduler.py:7-25), read by runners and hooks."""
+
     request_id: int
     prompt_tokens: int
     max_new_tokens: int
@@ -39,7 +54,52 @@ class ScheduleBatch:
     scheduled_tokens: int
 
 
+@dataclass(frozen=True)
+class PrefillPlan:
+    """What one prefill step does to the head of the queue.
+
+    ``examined`` requests form a prefix of the queue; ``grants[i]`` is the
+    number of prompt tokens request ``examined[i]`` receives (0 for one that
+    only moves to the running set). ``chunked`` is true when the last grant
+    leaves part of that prompt for a later step."""
+
+    examined: tuple[InferenceRequest, ...]
+    grants: tuple[int, ...]
+    chunked: bool
+
+    @property
+    def tokens(self) -> int:
+        return sum(self.grants)
+
+
+def plan_prefill(queue: Iterable[InferenceRequest], max_seqs: int, max_tokens: int) -> PrefillPlan:
+    """Token grants for one step over the queue head (pure: reads only)."""
+    examined: list[InferenceRequest] = []
+    grants: list[int] = []
+    taken = 0  # requests that received tokens
+    left = max_tokens
+    chunked = False
+    for request in queue:
+        if taken >= max_seqs or left <= 0:
+            break
+        need = request.prompt_remaining
+        if need and taken and need > left:
+            break  # only the step's first prompt may be cut short
+        give = min(need, left)
+        examined.append(request)
+        grants.append(give)
+        if give:
+            taken += 1
+            left -= give
+        if give < need:
+            chunked = True  # the budget is spent; this prompt resumes next step
+            break
+    return PrefillPlan(tuple(examined), tuple(grants), chunked)
+
+
 class TokenBudgetScheduler:
+    """FCFS scheduler with a per-step token budget (prefill first)."""
+
     def __init__(self, max_num_seqs: int = 32, max_num_batched_tokens: int = 2048):
         if max_num_seqs <= 0 or max_num_batched_tokens <= 0:
             raise ValueError("scheduler limits must be positive")
@@ -54,49 +114,45 @@ class TokenBudgetScheduler:
             raise ValueError("only waiting requests can be added")
         self.waiting.append(request)
 
-    def _admit(self, request: InferenceRequest) -> None:
-        request.status = "running"
-        self.running.append(request)
-
     def schedule(self) -> ScheduleBatch:
-        batch: list[InferenceRequest] = []
-        budget_used = 0
-        while self.waiting and len(batch) < self.max_num_seqs:
-            head = self.waiting[0]
-            budget_left = self.max_num_batched_tokens - budget_used
-            if budget_left <= 0:
-                break
-            need = head.prompt_remaining
-            if need == 0:
-                self.waiting.popleft()
-                self._admit(head)
-                continue
-            if batch and need > budget_left:
-                break
-            self.waiting.popleft()
-            take = min(need, budget_left)
-            head.cached_tokens += take
-            budget_used += take
-            batch.append(head)
-            if head.prompt_remaining == 0:
-                self._admit(head)
-            else:
-                head.status = "waiting"
-                self.waiting.appendleft(head)
-        if batch:
-            return ScheduleBatch(tuple(batch), "prefill", budget_used)
-        decode = tuple(self.running[: self.max_num_seqs])
-        if not decode:
-            return ScheduleBatch((), "idle", 0)
-        return ScheduleBatch(decode, "decode", len(decode))
+        plan = plan_prefill(self.waiting, self.max_num_seqs, self.max_num_batched_tokens)
+        prefilled = self._commit(plan)
+        if prefilled:
+            return ScheduleBatch(prefilled, "prefill", plan.tokens)
+        decoding = tuple(self.running[: self.max_num_seqs])
+        if decoding:
+            return ScheduleBatch(decoding, "decode", len(decoding))
+        return ScheduleBatch((), "idle", 0)
 
-    def mark_decode_step(self, requests) -> None:
-        stepped = {id(r) for r in requests}
-        for request in list(self.running):
-            if id(request) not in stepped:
-                continue
-            request.generated_tokens += 1
-            if request.finished:
-                request.status = "finished"
-                self.running.remove(request)
-                self.finished.append(request)
+    def _commit(self, plan: PrefillPlan) -> tuple[InferenceRequest, ...]:
+        """Applies a plan: grants become cached tokens, completed prompts join
+        the running set in queue order, a chunked prompt stays at the head."""
+        settled = len(plan.examined) - (1 if plan.chunked else 0)
+        for _ in range(settled):
+            self.waiting.popleft()
+        prefilled = []
+        for request, give in zip(plan.examined, plan.grants):
+            request.cached_tokens += give
+            if give:
+                prefilled.append(request)
+            if request.prompt_remaining:
+                request.status = "waiting"
+            else:
+                request.status = "running"
+                self.running.append(request)
+        return tuple(prefilled)
+
+    def mark_decode_step(self, requests: Sequence[InferenceRequest]) -> None:
+        """Counts one generated token for each running request of the step and
+        retires the ones that reached ``max_new_tokens``, in running order."""
+        stepped = {id(request) for request in requests}
+        still_running = []
+        for request in self.running:
+            if id(request) in stepped:
+                request.generated_tokens += 1
+                if request.finished:
+                    request.status = "finished"
+                    self.finished.append(request)
+                    continue
+            still_running.append(request)
+        self.running[:] = still_running

@@ -265,3 +265,37 @@ def test_runtime_rejects_two_prefill_hooks_and_duplicate_ids():
     runtime.submit(1, 2, 1)
     with pytest.raises(ValueError, match="duplicate"):
         runtime.submit(1, 2, 1)
+
+
+def test_scheduler_admits_empty_prompts_without_budget_and_caps_sequences():
+    """A request with nothing to prefill joins the running set in queue order
+    without using budget; at most max_num_seqs requests receive tokens per
+    step, and a later prompt that does not fit whole ends the step."""
+    scheduler = TokenBudgetScheduler(max_num_seqs=2, max_num_batched_tokens=8)
+    empty = InferenceRequest(0, 0, 1)
+    a, b, c = InferenceRequest(1, 3, 1), InferenceRequest(2, 3, 1), InferenceRequest(3, 1, 1)
+    for r in (empty, a, b, c):
+        scheduler.add(r)
+    first = scheduler.schedule()
+    assert first.phase == "prefill" and [r.request_id for r in first.requests] == [1, 2]
+    assert first.scheduled_tokens == 6 and [r.request_id for r in scheduler.running] == [0, 1, 2]
+    assert list(scheduler.waiting) == [c] and c.cached_tokens == 0
+    second = scheduler.schedule()
+    assert [r.request_id for r in second.requests] == [3] and second.scheduled_tokens == 1
+    decode = scheduler.schedule()
+    assert decode.phase == "decode" and [r.request_id for r in decode.requests] == [0, 1]
+    scheduler.mark_decode_step(decode.requests)
+    assert [r.request_id for r in scheduler.finished] == [0, 1]
+    assert [r.request_id for r in scheduler.running] == [2, 3]
+
+
+def test_scheduler_second_prompt_must_fit_whole():
+    scheduler = TokenBudgetScheduler(max_num_seqs=4, max_num_batched_tokens=5)
+    a, b = InferenceRequest(1, 3, 1), InferenceRequest(2, 4, 1)
+    scheduler.add(a)
+    scheduler.add(b)
+    first = scheduler.schedule()
+    assert [r.request_id for r in first.requests] == [1] and b.cached_tokens == 0
+    second = scheduler.schedule()  # b alone is first now: chunked at the budget
+    assert [r.request_id for r in second.requests] == [2] and b.cached_tokens == 4
+    assert b.status == "running"
