@@ -136,7 +136,12 @@ typedef struct ikl_paged_attention_args {
    * 64. */
   int32_t partition_size;
   /* Host-known upper bound of context_lens (0 = table_width*block_size);
-   * only sizes the grid, never read from device memory. */
+   * only sizes the grid, never read from device memory. Contract: every
+   * context_lens[b] <= max_context_len. The fixed partitions cover
+   * [0, max_context_len) only, so positions of a longer context past it are
+   * not attended (no fault, no error: the device lengths are not read on
+   * the host). The balanced split and the unsplit launch read the device
+   * lengths and are unaffected. */
   int64_t max_context_len;
   /* Kernel family: -1 = automatic (ikl_paged_attention_path), else an
    * enum ikl_attention_path value. */
@@ -310,6 +315,7 @@ typedef struct ikl_launch_config {
   int32_t split;               /* 0 = none, 1 = fixed partitions, 2 = balanced split */
   int32_t partition_size;      /* as ikl_paged_attention_partition_size */
   int64_t workgroups;          /* grid size of the attention kernel */
+  int32_t group_size;          /* query heads that share each K/V tile (one unit) */
 } ikl_launch_config;
 
 /* Launch configuration `args` resolves to, without launching. Replaces the

@@ -225,6 +225,7 @@ class LaunchConfig(ctypes.Structure):
         ("split", _c_i32),
         ("partition_size", _c_i32),
         ("workgroups", _c_i64),
+        ("group_size", _c_i32),
     ]
 
 

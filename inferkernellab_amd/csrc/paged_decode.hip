@@ -43,17 +43,12 @@ constexpr int pow2_divisor(int n, int cap) {
 
 constexpr int cmin(int a, int b) { return a < b ? a : b; }
 
-// Tuning knobs (compile-time): lanes per token cap for groups of <= 4 and
-// >= 8 heads, and 16-byte K (and V) loads per lane per tile.
-#ifndef IKL_TPT_CAP_SMALL_GROUP
-#define IKL_TPT_CAP_SMALL_GROUP 8
-#endif
-#ifndef IKL_TPT_CAP_LARGE_GROUP
-#define IKL_TPT_CAP_LARGE_GROUP 16
-#endif
-#ifndef IKL_LOADS_PER_LANE
-#define IKL_LOADS_PER_LANE 4
-#endif
+// Lanes per token: at most 8 for groups of <= 4 heads, 16 for groups of 8
+// (more lanes per token keep the per-lane query and accumulator registers
+// of a large group in budget); 16-byte K (and V) loads per lane per tile.
+constexpr int TPT_CAP_SMALL_GROUP = 8;
+constexpr int TPT_CAP_LARGE_GROUP = 16;
+constexpr int LOADS_PER_LANE = 4;
 
 template <typename Tag, int D, int G>
 struct ScalarCfg {
@@ -62,13 +57,13 @@ struct ScalarCfg {
   static constexpr int NCHUNK = D / VEC;           // chunks per head_dim row
   static_assert(D % VEC == 0, "head_dim must be a multiple of a 16-byte chunk");
   static constexpr int TPT =
-      pow2_divisor(NCHUNK, G >= 8 ? IKL_TPT_CAP_LARGE_GROUP : IKL_TPT_CAP_SMALL_GROUP);
+      pow2_divisor(NCHUNK, G >= 8 ? TPT_CAP_LARGE_GROUP : TPT_CAP_SMALL_GROUP);
   static constexpr int CPL = NCHUNK / TPT;         // chunks per lane
   static constexpr int LD = CPL * VEC;             // dims per lane
   static constexpr int ROWS = 64 / TPT;            // tokens per row-step
-  // Row-steps per tile: IKL_LOADS_PER_LANE chunks of K per lane, and never
+  // Row-steps per tile: LOADS_PER_LANE chunks of K per lane, and never
   // more than 64 tokens so one 64-entry block-table window covers a tile.
-  static constexpr int R0 = CPL >= IKL_LOADS_PER_LANE ? 1 : IKL_LOADS_PER_LANE / CPL;
+  static constexpr int R0 = CPL >= LOADS_PER_LANE ? 1 : LOADS_PER_LANE / CPL;
   static constexpr int R = cmin(R0, 64 / ROWS);
   static constexpr int TI = ROWS * R;              // tokens per tile (<= 64)
   static_assert(TI <= 64, "a tile must fit one table window");
@@ -519,13 +514,11 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
   pl.units = (int64_t)a->num_kv_heads * pl.groups_per_kv;
   const int64_t units = a->batch * pl.units;
 
-  // Balanced split waves: at least IKL_SK_MIN_TILES tiles each at the
+  // Balanced split waves: at least SK_MIN_TILES tiles each at the
   // longest context (a small batch runs fewer, longer waves, not one tile
   // each; e.g. MQA 32/1 hd64 B16 x 2048: 24.9 -> 16.5 us going from 1 to 4),
   // capped by the resident capacity.
-#ifndef IKL_SK_MIN_TILES
-#define IKL_SK_MIN_TILES 4
-#endif
+  constexpr int64_t SK_MIN_TILES = 4;
   // The balanced split on the MFMA family (one run of ~T/W tiles per
   // resident wave): asked for with partition_size = -2, and picked
   // automatically above SK_MIN_BATCH_TILES tiles at the longest context.
@@ -546,7 +539,7 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
       a->partition_size == -2 || (a->partition_size == 0 && pl.path == IKL_PATH_MFMA_GROUPED && t_max > SK_MIN_BATCH_TILES);
   if (want_balanced && cap < (int64_t(1) << 29)) {
     const int64_t w = std::min<int64_t>(mfma_streamk_capacity(a->dtype, a->head_dim, pl.group_size, pl.kv_fp8),
-                                        std::max<int64_t>((t_max + IKL_SK_MIN_TILES - 1) / IKL_SK_MIN_TILES, 1));
+                                        std::max<int64_t>((t_max + SK_MIN_TILES - 1) / SK_MIN_TILES, 1));
     if ((double)(t_max + 1) * (double)w < 4.0e18) {
       pl.sk_waves = (int)w;
       pl.split = true;
@@ -715,6 +708,7 @@ extern "C" int ikl_paged_attention_launch_config(const ikl_paged_attention_args 
   c.split = pl.sk_waves > 0 ? 2 : (pl.split ? 1 : 0);
   c.workgroups = pl.sk_waves > 0 ? (int64_t)pl.sk_waves
                                  : (int64_t)pl.num_parts * a->num_kv_heads * pl.groups_per_kv * a->batch;
+  c.group_size = pl.group_size;
   *out = c;
   return IKL_OK;
 }

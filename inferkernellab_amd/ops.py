@@ -101,9 +101,12 @@ def _as_index_tensor(value, device: torch.device) -> torch.Tensor:
     return value
 
 
-def _validate_attention(query, cache, block_tables, context_lens, layer, validate_inputs):
+def _validate_attention(query, cache, block_tables, context_lens, layer, validate_inputs,
+                        max_context_len=None):
     """Checks of triton_ops.py:415-457, in the same order with the same
-    messages; returns the table and length tensors."""
+    messages, plus this library's ``max_context_len`` hint (a bound of
+    ``context_lens`` that sizes the fixed-partition grid); returns the table
+    and length tensors."""
     if query.ndim != 3 or query.device.type != "cuda":
         raise ValueError("query must be a GPU (torch 'cuda' device) tensor with shape [B,H,D]")
     if query.shape[0] <= 0 or query.shape[1] <= 0 or query.shape[2] <= 0:
@@ -145,6 +148,8 @@ def _validate_attention(query, cache, block_tables, context_lens, layer, validat
             torch.any(block_tables >= layout.num_blocks).item()
         ):
             raise ValueError("block table contains an invalid physical block id")
+        if max_context_len and bool(torch.any(context_lens > max_context_len).item()):
+            raise ValueError("context length exceeds max_context_len")
     if query.dtype not in _DTYPES:
         raise ValueError("query dtype must be float16, bfloat16 or float32")
     return block_tables, context_lens
@@ -285,12 +290,15 @@ def launch_config(args) -> dict:
         "split": _SPLIT_NAMES[out.split],
         "partition_size": out.partition_size,
         "workgroups": out.workgroups,
+        "group_size": out.group_size,
     }
 
 
 def _record_launch(args) -> None:
     cfg = launch_config(args)
     _last_launch[cfg["path"]] = cfg
+    if cfg["path"] != "mha_fallback":
+        _last_launch["grouped"] = cfg  # the last launch of either grouped family
 
 
 def _reported(path: str) -> dict | None:
@@ -308,9 +316,15 @@ def paged_decode_autotune_config() -> dict | None:
 
 
 def paged_decode_grouped_autotune_config() -> dict | None:
-    """As :func:`paged_decode_autotune_config` for the VALU grouped kernel
-    (triton_ops.py:30-40)."""
-    return _reported("scalar_grouped")
+    """As :func:`paged_decode_autotune_config` for the most recent grouped
+    launch of either family, VALU or matrix-core (triton_ops.py:30-40).
+
+    The reference's callers pick the reporter by path name
+    (hf_benchmark.py:942-945, scripts/run_decode_sweep.py:249): the tl.dot
+    reporter for ``"tensorcore_short_context"``, this one otherwise. This
+    library's matrix-core path is named ``"mfma_grouped"``, so those callers
+    land here, and get the matrix-core launch they ran."""
+    return _reported("grouped")
 
 
 def paged_decode_grouped_dot_autotune_config() -> dict | None:
@@ -341,12 +355,14 @@ def paged_decode_attention_hip(
     partition; ``-1`` never splits, ``-2`` asks for the matrix-core
     family's balanced split, ``None`` picks automatically),
     ``max_context_len`` (a host-known bound of ``context_lens`` used to size
-    the split grid) and ``events`` (up to three raw hipEvent_t handles
+    the split grid: positions past it are not attended on the fixed
+    partitions, so with ``validate_inputs`` a longer context raises
+    ``ValueError``) and ``events`` (up to three raw hipEvent_t handles
     recorded before the attention kernel, after it and after the split
     reduce, for timing).
     """
     block_tables, context_lens = _validate_attention(
-        query, cache, block_tables, context_lens, layer, validate_inputs
+        query, cache, block_tables, context_lens, layer, validate_inputs, max_context_len
     )
     return _launch_attention(
         query,
@@ -387,7 +403,7 @@ def paged_decode_attention_hip_grouped(
     per group (MQA 32/1, batch 64: 66.7 µs with groups of 8 against 35.5 µs).
     """
     block_tables, context_lens = _validate_attention(
-        query, cache, block_tables, context_lens, layer, validate_inputs
+        query, cache, block_tables, context_lens, layer, validate_inputs, max_context_len
     )
     if query_group_size not in (1, 2, 4, 8):
         raise ValueError("query_group_size must be one of 1, 2, 4, or 8")
@@ -573,7 +589,7 @@ class PreparedPagedAttention:
                  max_context_len: int | None = None, validate_inputs: bool = True):
         self._lib = _require_backend()
         block_tables, context_lens = _validate_attention(
-            query, cache, block_tables, context_lens, layer, validate_inputs
+            query, cache, block_tables, context_lens, layer, validate_inputs, max_context_len
         )
         if not _aligned_rows(query):
             raise ValueError("query rows must be 16-byte aligned for a prepared launch")

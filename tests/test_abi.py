@@ -223,6 +223,60 @@ def test_autotune_reporters_are_none_before_a_launch():
     assert fresh.paged_decode_grouped_dot_autotune_config() is None
 
 
+def test_grouped_reporter_covers_the_matrix_core_path():
+    """The reference's callers ask paged_decode_grouped_autotune_config() for
+    every grouped path not named "tensorcore_short_context" (hf_benchmark.py:
+    942-945): it reports the last grouped launch of either family."""
+    import importlib
+
+    fresh = importlib.reload(ops)
+    fresh._record_launch(_args())  # bf16 GQA 32/8: matrix cores
+    dot = fresh.paged_decode_grouped_dot_autotune_config()
+    assert dot is not None and fresh.paged_decode_grouped_autotune_config() == dot
+    fresh._record_launch(_args(dtype=_lib.IKL_F32))  # fp32: the VALU grouped kernel
+    scalar = fresh.paged_decode_grouped_autotune_config()
+    assert scalar is not None and scalar != dot and scalar["num_warps"] == 1
+    assert fresh.paged_decode_grouped_dot_autotune_config() == dot
+    assert fresh.paged_decode_autotune_config() is None
+
+
+def _doc_structures(path: Path) -> dict:
+    """ctypes.Structure classes of the ```python blocks of a markdown file:
+    name -> [(field, ctypes type), ...] (parsed, not executed)."""
+    import ast
+
+    text = path.read_text()
+    found = {}
+    for block in re.findall(r"```python\n(.*?)```", text, flags=re.S):
+        for node in ast.walk(ast.parse(block)):
+            if not isinstance(node, ast.ClassDef):
+                continue
+            for stmt in node.body:
+                if isinstance(stmt, ast.Assign) and getattr(stmt.targets[0], "id", "") == "_fields_":
+                    fields = []
+                    for elt in stmt.value.elts:
+                        name, typ = elt.elts
+                        assert isinstance(typ, ast.Attribute) and typ.value.id == "ctypes"
+                        fields.append((name.value, getattr(ctypes, typ.attr)))
+                    found[node.name] = fields
+    return found
+
+
+def test_integration_stub_declares_every_struct_field():
+    """The binding INTEGRATION.md gives maintainers matches _lib.py (and so
+    the header) field for field, type for type."""
+    doc = _doc_structures(Path(__file__).resolve().parents[1] / "INTEGRATION.md")
+    assert "AppendArgs" in doc
+    for name, fields in doc.items():
+        cls = getattr(_lib, name)
+        assert fields == [(f, t) for f, t in cls._fields_], name
+
+        class Doc(ctypes.Structure):
+            _fields_ = fields
+
+        assert ctypes.sizeof(Doc) == ctypes.sizeof(cls), name
+
+
 def test_rope_append_rejects_bad_arguments_without_a_gpu():
     """ikl_rope_append_kv validates before launching: errors, not launches."""
     lib = _lib.load()

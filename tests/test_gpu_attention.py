@@ -419,3 +419,20 @@ def test_prepared_balanced_split_repeats_bit_identically(lengths, heads, kv):
         torch.cuda.synchronize()
         assert torch.equal(again.view(torch.int16), first.view(torch.int16))
     assert max_abs_err(first, case.expected()) <= ATOL["bfloat16"]
+
+
+def test_max_context_len_below_a_context_is_rejected():
+    """max_context_len sizes the fixed-partition grid; with validate_inputs a
+    context longer than it raises instead of being cut short."""
+    from inferkernellab_amd import ops
+
+    case = make_case(batch=2, num_heads=8, num_kv_heads=2, head_dim=128, block_size=16,
+                     lengths=[1500, 700], dtype="bfloat16", seed=52)
+    args = (case.device_query(), case.device_cache(), case.device_tables(), case.device_lengths())
+    with pytest.raises(ValueError, match="max_context_len"):
+        ops.paged_decode_attention_hip(*args, partition_size=512, max_context_len=1024)
+    with pytest.raises(ValueError, match="max_context_len"):
+        ops.PreparedPagedAttention(*args, partition_size=512, max_context_len=1024)
+    out = ops.paged_decode_attention_hip(*args, partition_size=512, max_context_len=1500)
+    torch.cuda.synchronize()
+    assert max_abs_err(out, case.expected()) <= ATOL["bfloat16"]
