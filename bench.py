@@ -48,6 +48,7 @@ import torch
 
 ROOT = Path(__file__).resolve().parent
 PEAK_HBM_GBPS = 8000.0
+PEAK_MFMA_TFLOPS = 2500.0  # MI355X dense bf16 / fp16 matrix peak
 METRIC = "paged decode attn µs/step + HBM GB/s (% peak), GQA 32/8 hd128 bf16"
 
 WORKLOADS = {
@@ -181,63 +182,144 @@ def step_bytes(w) -> tuple[int, int]:
     return attn, append
 
 
-def cpu_baseline(w, budget_s: float) -> dict:
-    """Times the CPU oracle (numpy paged_reference) on the requests of the
-    same workload, cycling through the batch until ~budget_s of CPU work,
-    then scales the mean per-request time to one step."""
-    import numpy as np
-    from oracle import paged_oracle as po
+# Tolerances of this path against the fp32 oracle (max-abs), plus half an
+# ulp of the output dtype at |expected| for the output's own rounding.
+TOLERANCE = {torch.float16: 2e-3, torch.bfloat16: 1e-2, torch.float32: 1e-4}
+_SIGNIFICAND_BITS = {torch.float16: 11, torch.bfloat16: 8, torch.float32: 24}
 
+
+def host_threads() -> int:
     try:
         from threadpoolctl import threadpool_info
 
-        threads = max([info.get("num_threads", 1) for info in threadpool_info()] or [1])
+        return max([info.get("num_threads", 1) for info in threadpool_info()] or [1])
     except Exception:  # pragma: no cover
-        threads = os.cpu_count() or 1
+        return os.cpu_count() or 1
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def oracle_view(w):
+    """(OracleCache over a host copy of the workload's cache, fp32 query) for
+    the CPU oracle. The FP8 cache is attended dequantised (codes x scales,
+    exact in fp32)."""
+    import numpy as np
+    from oracle import paged_oracle as po
+
     cache = w["cache"]
     dtype = {torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32"}[w["dtype"]]
-    oc = po.OracleCache.__new__(po.OracleCache)
-    oc.num_layers, oc.num_blocks, oc.block_size = 1, w["pool"], w["block_size"]
-    oc.num_kv_heads, oc.head_dim, oc.dtype = w["kv_heads"], w["head_dim"], dtype
 
     def host(t):
         t = t.detach().cpu()
         return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
 
-    if w["fp8"]:  # the oracle attends the dequantised cache
-        oc.dtype = "float32"
-        oc.k = (cache.k.float() * cache.k_scale.transpose(2, 3).unsqueeze(-1)).cpu().numpy()
-        oc.v = (cache.v.float() * cache.v_scale.transpose(2, 3).unsqueeze(-1)).cpu().numpy()
+    if w["fp8"]:
+        k = (cache.k.float() * cache.k_scale.transpose(2, 3).unsqueeze(-1)).cpu().numpy()
+        v = (cache.v.float() * cache.v_scale.transpose(2, 3).unsqueeze(-1)).cpu().numpy()
+        oc = po.OracleCache.wrap(k, v, "float32")
     else:
-        oc.k, oc.v = host(cache.k), host(cache.v)
-    q = po.to_f32(host(w["query"]), dtype)
-    done, elapsed, kv_bytes, ctx_tokens = 0, 0.0, 0, 0
-    eb = cache.k.element_size()
-    batch = len(w["lengths"])
-    while elapsed < budget_s:
-        b = done % batch
-        t0 = time.perf_counter()
-        po.paged_decode_attention(q[b : b + 1], oc, [w["tables_list"][b]], [w["lengths"][b]])
-        elapsed += time.perf_counter() - t0
-        kv_bytes += w["lengths"][b] * w["kv_heads"] * w["head_dim"] * 2 * eb
-        ctx_tokens += w["lengths"][b]
-        done += 1
-    # per-token cost scaled to the step's context tokens
-    step_s = elapsed / ctx_tokens * sum(w["lengths"])
+        oc = po.OracleCache.wrap(host(cache.k), host(cache.v), dtype)
+    return oc, po.to_f32(host(w["query"]), dtype)
+
+
+def oracle_step(view, w):
+    """The oracle's paged_reference over every request of the step: fp32 [B, H, D]."""
+    from oracle import paged_oracle as po
+
+    oc, q = view
+    return po.paged_decode_attention(q, oc, w["tables_list"], w["lengths"])
+
+
+def parity(out: torch.Tensor, expected, dtype: torch.dtype) -> dict:
+    """Max-abs error of the kernel output against the oracle and the largest
+    excess over the tolerance (<= 0 passes): |out - expected| <= tol + half
+    an ulp of the output dtype at |expected|."""
+    import numpy as np
+
+    got = out.detach().float().cpu().numpy()
+    err = np.abs(got - expected)
+    _, e = np.frexp(np.abs(expected).astype(np.float64))
+    half_ulp = np.ldexp(1.0, e - _SIGNIFICAND_BITS[dtype] - 1)
+    excess = float(np.max(err - (TOLERANCE[dtype] + half_ulp))) if err.size else 0.0
     return {
-        "value": round(step_s * 1e6, 1),
-        "unit": "us/step",
-        "gbps": round(kv_bytes / elapsed / 1e9, 3),
-        "cores": threads,
-        "kind": "port",
-        "sample": f"oracle paged_reference (numpy fp32), {done} single-request attentions cycling "
-                  f"through the {batch} requests ({ctx_tokens} context tokens, {elapsed:.1f} s), "
-                  f"scaled per context token to the full step",
+        "max_abs_err": float(np.max(err)) if err.size else 0.0,
+        "tolerance": TOLERANCE[dtype],
+        "max_excess": excess,
+        "nan": bool(np.isnan(got).any()),
+        "passed": bool(excess <= 0 and not np.isnan(got).any()),
     }
 
 
+def cpu_baseline(w, view, budget_s: float, first_step_s: float) -> dict:
+    """Times the CPU oracle (numpy paged_reference) over whole decode steps of
+    the same workload — every request of the batch per step — until about
+    budget_s of CPU work; the parity check's step is the first sample."""
+    samples = [first_step_s]
+    while sum(samples) < budget_s:
+        t0 = time.perf_counter()
+        oracle_step(view, w)
+        samples.append(time.perf_counter() - t0)
+    step_s = sum(samples) / len(samples)
+    kv_bytes = sum(w["lengths"]) * w["kv_heads"] * w["head_dim"] * 2 * w["cache"].k.element_size()
+    return {
+        "value": round(step_s * 1e6, 1),
+        "unit": "us/step",
+        "gbps": round(kv_bytes / step_s / 1e9, 3),
+        "cores": host_threads(),
+        "cpu": cpu_model(),
+        "logical_cpus": os.cpu_count(),
+        "kind": "port",
+        "sample": f"oracle paged_reference (numpy fp32 per-request loop): {len(samples)} whole steps "
+                  f"of all {len(w['lengths'])} requests ({sum(w['lengths'])} context tokens each, "
+                  f"{sum(samples):.1f} s), mean per step",
+    }
+
+
+def mfma_figures(w, attn, kernel_ms: float, workload: str) -> dict | None:
+    """Matrix-core use of the decode kernel (MFMA family only): the flops
+    the attention needs (QK^T and PV, 4 * head_dim per context token and
+    query head), the flops the MFMA instructions issue (16-token tiles x
+    16-head groups, PV twice for bf16 P with its residual), both as rates
+    over the kernel time against the dense bf16/fp16 peak, and the MFMA
+    busy share measured by rocprofv3 counters when a profile of the
+    workload holds it."""
+    if attn.path != "mfma_grouped":
+        return None
+    lengths, d = w["lengths"], w["head_dim"]
+    heads_per_kv = w["heads"] // w["kv_heads"]
+    group = attn.launch["group_size"]
+    units = w["kv_heads"] * -(-heads_per_kv // group)
+    ng = 1 if group <= 16 else 2
+    tiles = units * sum(-(-n // 16) for n in lengths)
+    pv_passes = 2 if (w["dtype"] == torch.bfloat16 and not w["fp8"]) else 1
+    issued = tiles * (2 * 16 * 16 * ng * d) * (1 + pv_passes)
+    needed = 4 * d * w["heads"] * sum(lengths)
+    secs = kernel_ms * 1e-3
+    out = {
+        "peak_tflops": PEAK_MFMA_TFLOPS,
+        "algorithmic_tflops": round(needed / secs / 1e12, 2),
+        "issued_tflops": round(issued / secs / 1e12, 2),
+        "frac_issued_of_peak": round(issued / secs / 1e12 / PEAK_MFMA_TFLOPS, 4),
+        "busy_frac": None,
+    }
+    prof = ROOT / "profiles" / f"mfma_{workload}.json"
+    if prof.exists():
+        try:
+            out["busy_frac"] = json.loads(prof.read_text()).get("mfma_busy_frac")
+        except (OSError, ValueError):
+            pass
+    return out
+
+
 # ------------------------------------------------------------------ prefill
-PEAK_MFMA_TFLOPS = 2500.0  # MI355X dense bf16 / fp16 matrix peak
 PREFILL_METRIC = "paged prefill attention TFLOP/s (causal, algorithmic flops), bf16"
 PREFILL_WORKLOADS = {
     # name: (batch, heads, kv_heads, head_dim, dtype, chunk start, chunk end) — every request
@@ -310,29 +392,55 @@ def torch_gather_sdpa(w):
                                           attn_mask=allow.unsqueeze(1), enable_gqa=True)
 
 
+def prefill_oracle_view(w):
+    """(OracleCache over a host copy of the prefill workload's cache, fp32 query)."""
+    import numpy as np
+    from oracle import paged_oracle as po
+
+    dtype = {torch.bfloat16: "bfloat16", torch.float16: "float16"}[w["dtype"]]
+
+    def host(t):
+        t = t.detach().cpu()
+        return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
+
+    return po.OracleCache.wrap(host(w["cache"].k), host(w["cache"].v), dtype), po.to_f32(host(w["query"]), dtype)
+
+
+def prefill_parity(w, out: torch.Tensor, rows: int = 64) -> dict:
+    """The kernel's output against the oracle on a bounded sample: for every
+    request, the first and the last `rows` query rows of its chunk (the
+    shortest and the longest prefixes), all heads."""
+    import numpy as np
+    from oracle import paged_oracle as po
+
+    oc, q = prefill_oracle_view(w)
+    worst = {"max_abs_err": 0.0, "tolerance": TOLERANCE[w["dtype"]], "max_excess": -1.0, "nan": False,
+             "passed": True}
+    checked = 0
+    for b in range(q.shape[0]):
+        span = w["ends"][b] - w["starts"][b]
+        for r0 in sorted({0, max(0, span - rows)}):
+            r1 = min(span, r0 + rows)
+            s = w["starts"][b] + r0
+            exp = po.paged_prefill_attention(q[b : b + 1, :, r0:r1], oc, [w["tables_list"][b]], [s],
+                                             [w["starts"][b] + r1])
+            res = parity(out[b : b + 1, :, r0:r1], exp, w["dtype"])
+            worst["max_abs_err"] = max(worst["max_abs_err"], res["max_abs_err"])
+            worst["max_excess"] = max(worst["max_excess"], res["max_excess"])
+            worst["nan"] = worst["nan"] or res["nan"]
+            worst["passed"] = worst["passed"] and res["passed"]
+            checked += r1 - r0
+    worst["checked"] = f"{checked} query rows x {q.shape[1]} heads (first and last {rows} rows of every chunk)"
+    return worst
+
+
 def prefill_cpu_baseline(w, budget_s: float) -> dict:
     """Times the CPU oracle's paged_prefill_attention on 256-row slices of the
     workload's chunks (cycling through requests and slices) for ~budget_s,
     then scales per attended (row, key) pair to the whole launch."""
-    import numpy as np
     from oracle import paged_oracle as po
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max([info.get("num_threads", 1) for info in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover
-        threads = os.cpu_count() or 1
-    dtype = {torch.bfloat16: "bfloat16", torch.float16: "float16"}[w["dtype"]]
-    oc = po.OracleCache.__new__(po.OracleCache)
-    oc.num_layers, oc.num_blocks, oc.block_size = 1, w["pool"], w["block_size"]
-    oc.num_kv_heads, oc.head_dim, oc.dtype = w["kv_heads"], w["head_dim"], dtype
-
-    def host(t):
-        return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
-
-    oc.k, oc.v = host(w["cache"].k), host(w["cache"].v)
-    q = po.to_f32(host(w["query"]), dtype)
+    oc, q = prefill_oracle_view(w)
     batch, width = q.shape[0], q.shape[2]
     rows = min(256, width)
     slices = [(b, r0) for r0 in range(0, width, rows) for b in range(batch)]
@@ -350,7 +458,9 @@ def prefill_cpu_baseline(w, budget_s: float) -> dict:
     return {
         "value": round(step_s * 1e6, 1),
         "unit": "us/step",
-        "cores": threads,
+        "cores": host_threads(),
+        "cpu": cpu_model(),
+        "logical_cpus": os.cpu_count(),
         "kind": "port",
         "sample": f"oracle paged_prefill_attention (numpy fp32), {done} slices of <= {rows} rows "
                   f"({pairs} attended row-key pairs per head, {elapsed:.1f} s), scaled per attended "
@@ -369,6 +479,14 @@ def run_prefill(args, device) -> int:
     events = HipEvents()
     k_steps, warmup = args.steps, args.warmup
     ev = [[events.create() for _ in range(2)] for _ in range(k_steps)]
+    # correctness gate before timing (the reference's harness raises on a
+    # mismatch before it times, benchmark.py:225-268)
+    prep(q, 0, out=out)
+    torch.cuda.synchronize()
+    check = prefill_parity(w, out)
+    if not check["passed"]:
+        print(json.dumps({"error": "prefill kernel output differs from the oracle", "parity": check}))
+        return 3
     for _ in range(warmup):
         prep(q, 0, out=out)
     torch.cuda.synchronize()
@@ -442,6 +560,7 @@ def run_prefill(args, device) -> int:
         "algorithmic_flops_per_launch": flops,
         "torch_gather_sdpa_us": round(sdpa_ms * 1e3, 1) if sdpa_ms is not None else None,
         "max_abs_diff_vs_torch_sdpa": err,
+        "parity": check,
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved, 1),
@@ -540,6 +659,23 @@ def main() -> int:
         flush_marks.clear()
         return t
 
+    # Correctness gate before timing, like the reference's harness
+    # (benchmark.py:225-268, which raises when the kernel differs from its
+    # PyTorch reference): one eager step, every request against the oracle.
+    attn()
+    torch.cuda.synchronize()
+    view = oracle_view(w)
+    t_oracle = time.perf_counter()
+    expected = oracle_step(view, w)
+    first_oracle_s = time.perf_counter() - t_oracle
+    check = parity(attn.out, expected, w["dtype"])
+    check["checked"] = f"all {len(w['lengths'])} requests x {w['heads']} heads of one eager step"
+    if not check["passed"]:
+        print(json.dumps({"error": "decode attention output differs from the oracle", "parity": check}))
+        return 3
+    checked_out = attn.out.clone()
+    append()
+
     # Eager pass: HIP events recorded around the split kernel and the reduce
     # on their stream (the roofline's kernel time). With the MALL flush, the
     # flush runs before each sample, outside the brackets, and its time is
@@ -580,6 +716,15 @@ def main() -> int:
         torch.cuda.synchronize()
         wall_s = time.perf_counter() - t0 - flush_seconds()
         step_mode = "hip graph replay"
+    torch.cuda.synchronize()
+    # every timed step recomputes the checked output (same inputs; the
+    # append writes past each context): the last one must equal it bit for bit
+    check["timed_steps_equal_checked_step"] = bool(torch.equal(attn.out.view(torch.int16) if attn.out.element_size() == 2
+                                                               else attn.out, checked_out.view(torch.int16)
+                                                               if checked_out.element_size() == 2 else checked_out))
+    if not check["timed_steps_equal_checked_step"]:
+        print(json.dumps({"error": "timed steps changed the attention output", "parity": check}))
+        return 3
     kernel_ms = [events.elapsed_ms(e[0], e[1]) for e in ev]
     reduce_ms = [events.elapsed_ms(e[1], e[2]) for e in ev]
     for trio in ev:
@@ -603,7 +748,7 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(w, args.cpu_budget_s)
+        cpu = cpu_baseline(w, view, args.cpu_budget_s, first_oracle_s)
 
     record = {
         "metric": METRIC,
@@ -655,6 +800,8 @@ def main() -> int:
             "kernel": attn.kernel_names()[0],
             "algorithmic_bytes_per_launch": attn_bytes,
         },
+        "mfma": mfma_figures(w, attn, kern_avg_ms, args.workload),
+        "parity": check,
         "cpu_baseline": cpu,
     }
     print(json.dumps(record))

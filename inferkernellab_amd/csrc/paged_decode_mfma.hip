@@ -36,44 +36,21 @@ namespace {
 
 constexpr int TILE = 16;  // tokens per tile
 
-// Build-time knobs; the defaults are the measured best:
-//   IKL_MFMA_SPLIT_P     bf16 P enters the PV product with its rounding
-//                        residual in a second MFMA (below);
-//   IKL_MFMA_HEAD_MAJOR  fixed partitions: the kv heads of one partition
-//                        are dispatched together;
-//   IKL_MFMA_PREFETCH    tiles in flight ahead of the one computing (1 or 2);
-//   IKL_MFMA_MIN_WAVES   one minimum waves-per-SIMD request for every kernel
-//                        (unset: the per-kernel choice below).
-#ifndef IKL_MFMA_SPLIT_P
-#define IKL_MFMA_SPLIT_P 1
-#endif
-#ifndef IKL_MFMA_HEAD_MAJOR
-#define IKL_MFMA_HEAD_MAJOR 1
-#endif
-#ifndef IKL_MFMA_PREFETCH
-#define IKL_MFMA_PREFETCH 1
-#endif
-// Register budget: at least MIN waves per SIMD, so VGPRs + AGPRs <= 512 / MIN.
-// The FP8 kernels with 16-head units ask for 2: they then keep their
-// accumulators in VGPRs, without the accumulator-register copies the
-// compiler otherwise places in every tile (81 -> 78 us on the FP8 GQA decode
-// workload). The others keep the compiler's choice (the 32-head kernels
-// would spill; the 16-bit 16-head one measured no better).
-#ifndef IKL_MFMA_MIN_WAVES
+// Register budget: the FP8 kernels with 16-head units ask for at least 2
+// waves per SIMD (VGPRs + AGPRs <= 256): they then keep their accumulators
+// in VGPRs, without the accumulator-register copies the compiler otherwise
+// places in every tile (81 -> 78 us on the FP8 GQA decode workload). The
+// others keep the compiler's choice (the 32-head kernels would spill; the
+// 16-bit 16-head one measured no better).
 #define IKL_MFMA_WAVES_ATTR __attribute__((amdgpu_waves_per_eu(KV8 && NG == 1 ? 2 : 1, 8)))
-#else
-#define IKL_MFMA_WAVES_ATTR __attribute__((amdgpu_waves_per_eu(IKL_MFMA_MIN_WAVES, 8)))
-#endif
 
-// bf16 P with its rounding residual in a second MFMA (fp16 P is not split).
-// The FP8 cache skips it: its values carry 4 significant bits, far below
-// what the residual would add.
-#ifndef IKL_MFMA_SPLIT_P_FP8
-#define IKL_MFMA_SPLIT_P_FP8 0
-#endif
+// bf16 P enters the PV product with its rounding residual in a second MFMA
+// (fp16 P, <= 2^8, already keeps 11 bits and is not split). The FP8 cache
+// skips it: its values carry 4 significant bits, far below what the
+// residual would add.
 template <typename Tag, bool KV8 = false>
 constexpr bool split_p() {
-  return (KV8 ? IKL_MFMA_SPLIT_P_FP8 : IKL_MFMA_SPLIT_P) != 0 && mfma_ops<Tag>::NARROW_P;
+  return !KV8 && mfma_ops<Tag>::NARROW_P;
 }
 
 // Two E4M3 codes -> two bf16 / fp16 values (exact: every E4M3 value is a
@@ -353,21 +330,7 @@ struct WaveTiles {
       }
     };
 
-    // software pipeline: the loads of the next IKL_MFMA_PREFETCH tiles fly
-    // while a tile computes
-#if IKL_MFMA_PREFETCH == 2
-    Tile ta, tb, tc;
-    issue(0, ta);
-    issue(1, tb);
-    for (int t = 0; t < n_tiles; t += 3) {
-      issue(t + 2, tc);
-      compute(ta);
-      issue(t + 3, ta);
-      if (t + 1 < n_tiles) compute(tb);
-      issue(t + 4, tb);
-      if (t + 2 < n_tiles) compute(tc);
-    }
-#else
+    // software pipeline: the next tile's loads fly while a tile computes
     Tile ta, tb;
     issue(0, ta);
     for (int t = 0; t < n_tiles; t += 2) {
@@ -376,7 +339,6 @@ struct WaveTiles {
       issue(t + 2, ta);
       if (t + 1 < n_tiles) compute(tb);
     }
-#endif
     // combine the four lane groups' sums (m is already common to them)
 #pragma unroll
     for (int g = 0; g < NG; ++g) lsum[g] = sum_xor32(sum_xor16(lsum[g]));
@@ -439,15 +401,10 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
   __shared__ float lds_m[WAVES][NH], lds_l[WAVES][NH];
 
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-#if IKL_MFMA_HEAD_MAJOR
+  // head-major grid: the units of one partition are dispatched together
   const int part = blockIdx.y;
   const int kvh = blockIdx.x / p.groups_per_kv;
   const int qg = blockIdx.x % p.groups_per_kv;
-#else
-  const int part = blockIdx.x;
-  const int kvh = blockIdx.y / p.groups_per_kv;
-  const int qg = blockIdx.y % p.groups_per_kv;
-#endif
   const int64_t b = blockIdx.z;
 
   const int64_t ctx = p.lens_i64 ? load_index<int64_t>(p.lens, b) : load_index<int32_t>(p.lens, b);
@@ -622,14 +579,11 @@ __global__ __launch_bounds__(64) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_stre
   }
 }
 
-#ifndef IKL_MFMA_WG_WAVES
-#define IKL_MFMA_WG_WAVES 4
-#endif
 // Waves sharing one fixed partition: 4 for 16-head units; 2 for 32-head
 // units (their staged [32 x D] blocks would exceed 64 KB of LDS at 4).
 template <int NG>
 constexpr int wg_waves() {
-  return NG == 1 ? IKL_MFMA_WG_WAVES : 2;
+  return NG == 1 ? 4 : 2;
 }
 
 template <typename Tag, int D, int NG, bool KV8>
@@ -638,9 +592,7 @@ void launch_shape(const AttnParams &p, dim3 grid, hipStream_t s) {
     paged_decode_mfma_streamk_kernel<Tag, D, NG, KV8><<<dim3((unsigned)p.sk_waves), 64, 0, s>>>(p);
     return;
   }
-#if IKL_MFMA_HEAD_MAJOR
-  grid = dim3(grid.y, grid.x, grid.z);
-#endif
+  grid = dim3(grid.y, grid.x, grid.z);  // head-major: (unit, partition, request)
   constexpr int WAVES = wg_waves<NG>();
   paged_decode_mfma_kernel<Tag, D, NG, WAVES, KV8><<<grid, dim3(64 * WAVES), 0, s>>>(p);
 }
@@ -725,7 +677,7 @@ hipError_t launch_mfma_attention(int dtype, int head_dim, const AttnParams &p, d
 
 MfmaShape mfma_launch_shape(bool balanced, int group_size) {
   const int waves = group_size > 16 ? wg_waves<2>() : wg_waves<1>();
-  return MfmaShape{TILE, balanced ? 1 : waves, IKL_MFMA_PREFETCH + 1};
+  return MfmaShape{TILE, balanced ? 1 : waves, 2};
 }
 
 int mfma_streamk_capacity(int dtype, int head_dim, int group_size, bool kv_fp8) {

@@ -109,24 +109,14 @@ __device__ inline int64_t pf_logical(const PrefillParams &p, int64_t pos) {
 constexpr int PT = 32;     // keys per tile
 constexpr int PWAVES = 4;  // waves per workgroup
 
-// Tuning knobs: 16-row MFMA groups per wave (NG), bf16 P split into two
-// MFMAs, tiles fetched ahead, and the register budget as waves per SIMD.
-// Measured on 8 x 4096-token GQA-32/8 prompts: NG = 2 at 2 waves/SIMD
-// beats NG = 4 at 1 wave/SIMD (1.49 vs 2.14 ms); fetching two tiles ahead
-// gains ~3 %; the split P costs ~13 % for no accuracy the bf16 bound needs.
-#ifndef IKL_PREFILL_NG
-#define IKL_PREFILL_NG 2
-#endif
-#ifndef IKL_PREFILL_SPLIT_P
-#define IKL_PREFILL_SPLIT_P 0
-#endif
-#ifndef IKL_PREFILL_PREFETCH
-#define IKL_PREFILL_PREFETCH 2
-#endif
-#ifndef IKL_PREFILL_MIN_WAVES
-#define IKL_PREFILL_MIN_WAVES 2
-#endif
-#define IKL_PREFILL_WAVES_ATTR __attribute__((amdgpu_waves_per_eu(IKL_PREFILL_MIN_WAVES, 8)))
+// 16-row MFMA groups per wave and register budget, measured on 8 x
+// 4096-token GQA-32/8 prompts: two groups at 2 waves/SIMD beat four at 1
+// wave/SIMD (1.49 vs 2.14 ms); fetching two tiles ahead gains ~3 % over
+// one; bf16 P is not split into a second MFMA (that cost ~13 % for
+// accuracy the bf16 bound does not need).
+constexpr int PREFILL_NG = 2;
+constexpr int PF = 2;  // tiles fetched ahead
+#define IKL_PREFILL_WAVES_ATTR __attribute__((amdgpu_waves_per_eu(2, 8)))
 
 // Two E4M3 codes times one fp32 scale -> two 16-bit values (one rounding).
 template <typename Tag>
@@ -150,7 +140,6 @@ template <typename Tag, int D, int NG, bool KV8>
 __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_prefill_mfma_kernel(const PrefillParams p) {
   static_assert(D % 32 == 0 && D <= 128, "MFMA prefill needs head_dim = 32k <= 128");
   using ops = mfma_ops<Tag>;
-  constexpr bool SPLIT = IKL_PREFILL_SPLIT_P != 0 && ops::NARROW_P;
   constexpr int EB = 2;
   constexpr int ROWB = D * EB;               // bytes per K/V row
   constexpr int PIECES = ROWB / 16;          // 16-byte pieces per row
@@ -159,7 +148,6 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
   constexpr int RW = 16 * NG;                // query rows per wave
   constexpr int RWG = RW * PWAVES;           // query rows per workgroup
   constexpr int TILE_BYTES = PT * ROWB;      // one staged K or V tile
-  constexpr int PF = IKL_PREFILL_PREFETCH;   // tiles fetched ahead
   constexpr int CEB = KV8 ? 1 : EB;          // bytes per cache element
   constexpr int CPIECES = D * CEB / 16;      // 16-byte pieces per cache row
   constexpr int PPL = (16 * CPIECES + 63) / 64;  // copy pieces per lane (a wave moves a half tile)
@@ -376,7 +364,7 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
         s1[g] = ops::mma_k32(ka[1][s], qb[g][s], s1[g]);
       }
     }
-    v4u32 pb[NG], pl[NG];
+    v4u32 pb[NG];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       // lane: row hl of group g, keys 8 grp + j (j < 4 from s0, 4.. from s1);
@@ -421,23 +409,13 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
       pb[g] = v4u32{ops::pack(pr[0], pr[1]), ops::pack(pr[2], pr[3]), ops::pack(pr[4], pr[5]),
                     ops::pack(pr[6], pr[7])};
       lacc[g] = ops::mma_k32(ones, pb[g], lacc[g]);
-      if constexpr (SPLIT) {
-        pl[g] = v4u32{ops::pack(pr[0] - ops::lo(pb[g].x), pr[1] - ops::hi(pb[g].x)),
-                      ops::pack(pr[2] - ops::lo(pb[g].y), pr[3] - ops::hi(pb[g].y)),
-                      ops::pack(pr[4] - ops::lo(pb[g].z), pr[5] - ops::hi(pb[g].z)),
-                      ops::pack(pr[6] - ops::lo(pb[g].w), pr[7] - ops::hi(pb[g].w))};
-        lacc[g] = ops::mma_k32(ones, pl[g], lacc[g]);
-      }
     }
 #pragma unroll
     for (int mt = 0; mt < MTILES; ++mt) {
       const u32x2_t v0 = lds_read_tr(vt + tr_off[0][mt]), v1 = lds_read_tr(vt + tr_off[1][mt]);
       const v4u32 va = v4u32{v0.x, v0.y, v1.x, v1.y};  // V^T[16mt + hl][keys 8 grp .. +7]
 #pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        acc[g][mt] = ops::mma_k32(va, pb[g], acc[g][mt]);
-        if constexpr (SPLIT) acc[g][mt] = ops::mma_k32(va, pl[g], acc[g][mt]);
-      }
+      for (int g = 0; g < NG; ++g) acc[g][mt] = ops::mma_k32(va, pb[g], acc[g][mt]);
     }
   };
 
@@ -474,7 +452,6 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
     if (j + PF < n_tiles) fetch(j + PF, T);
     compute(kt, vt, j * PT, holes_t);
   };
-#if IKL_PREFILL_PREFETCH == 2
   Staged ta, tb;
   if (n_tiles > 0) fetch(0, ta);
   if (n_tiles > 1) fetch(1, tb);
@@ -482,11 +459,6 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
     step(j, ta);
     if (j + 1 < n_tiles) step(j + 1, tb);
   }
-#else
-  Staged ta;
-  if (n_tiles > 0) fetch(0, ta);
-  for (int j = 0; j < n_tiles; ++j) step(j, ta);
-#endif
 
   // Normalise and store. Lane (hl, grp) holds O^T[16 mt + 4 grp + i][row hl].
   float lsum[NG];
@@ -778,7 +750,7 @@ extern "C" int ikl_paged_prefill_attention(const ikl_paged_prefill_args *a, void
   if (ev0 && hipEventRecord(ev0, s) != hipSuccess) return check_launch("ikl_paged_prefill_attention: event record");
   hipError_t err;
   if (path == IKL_PATH_MFMA_GROUPED) {
-    constexpr int NG = IKL_PREFILL_NG;
+    constexpr int NG = PREFILL_NG;
     const int64_t rows = a->query_width * p.heads_per_kv;
     constexpr int64_t rows_per_wg = 16 * NG * PWAVES;  // RWG of the kernel
     p.row_blocks = (rows + rows_per_wg - 1) / rows_per_wg;

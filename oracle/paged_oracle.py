@@ -133,6 +133,20 @@ class OracleCache:
         self.k = np.full(shape, init, dtype=sd)
         self.v = np.full(shape, init, dtype=sd)
 
+    @classmethod
+    def wrap(cls, k: np.ndarray, v: np.ndarray, dtype: str) -> "OracleCache":
+        """A cache over existing storage arrays ``[layers, blocks, block_size,
+        kv_heads, head_dim]`` (no copy), e.g. a device cache copied to host."""
+        if k.shape != v.shape or k.ndim != 5:
+            raise ValueError("k/v must share a [L, NB, bs, Hkv, D] shape")
+        if dtype not in DTYPES or k.dtype != storage_dtype(dtype) or v.dtype != k.dtype:
+            raise ValueError(f"storage arrays do not hold {dtype}")
+        self = cls.__new__(cls)
+        self.num_layers, self.num_blocks, self.block_size, self.num_kv_heads, self.head_dim = k.shape
+        self.dtype = dtype
+        self.k, self.v = k, v
+        return self
+
     def slot_mapping(self, block_table, start: int, length: int) -> np.ndarray:
         """slot(p) = table[p // bs] * bs + p % bs for p in [start, start+length)."""
         if start < 0 or length < 0:
