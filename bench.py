@@ -591,6 +591,9 @@ def main() -> int:
     parser.add_argument("--kv-layout", choices=("default", "token-major", "head-major"), default="default",
                         help="cache block layout: [block_size, kv_heads, D] (the reference's, default for "
                              "16-bit caches) or [kv_heads, block_size, D] (default for the FP8 cache)")
+    parser.add_argument("--separate-append", action="store_true",
+                        help="launch the append as its own kernel after the attention instead of "
+                             "letting the split reduce kernel carry it (same result)")
     parser.add_argument("--no-graph", action="store_true",
                         help="time eager launches instead of HIP graph replays of the step")
     parser.add_argument("--mall-flush", choices=("auto", "on", "off"), default="auto",
@@ -635,6 +638,18 @@ def main() -> int:
         partition_size=partition, max_context_len=max(w["lengths"]),
     )
     append = ops.PreparedAppend(w["new_k"], w["new_v"], w["cache"], w["slots"])
+    step = ops.PreparedDecodeStep(attn, append)
+
+    def run_step(events=None) -> None:
+        """Attention then the 1-token append: one library call (the append
+        rides on the split reduce kernel when it can), or with
+        --separate-append the two operators launched one after the other."""
+        if args.separate_append:
+            attn(events=events)
+            append()
+        else:
+            step(events=events)
+
     events = HipEvents()
     k_steps, warmup = args.steps, args.warmup
     ev = [[events.create() for _ in range(3)] for _ in range(k_steps)]
@@ -681,41 +696,61 @@ def main() -> int:
     # flush runs before each sample, outside the brackets, and its time is
     # taken out of the wall time.
     for _ in range(warmup):
-        attn()
-        append()
+        run_step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(k_steps):
         flush_mall(i)
-        attn(events=ev[i])
-        append()
+        run_step(events=ev[i])
     torch.cuda.synchronize()
     wall_s = eager_wall_s = time.perf_counter() - t0 - flush_seconds()
     step_mode = "eager launches"
+    single_graph_us = None
     if not args.no_graph:
-        # The step (split kernel, reduce, append) captured once as a HIP
-        # graph and replayed: a decode loop's launch pattern, without the
-        # host's per-kernel dispatch gaps. Timed: exactly K replays.
-        side = torch.cuda.Stream(device)
-        side.wait_stream(torch.cuda.current_stream(device))
-        with torch.cuda.stream(side):
-            attn()
-            append()
-        torch.cuda.current_stream(device).wait_stream(side)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            attn()
-            append()
+        # HIP graphs: a decode loop's launch pattern, without the host's
+        # per-kernel dispatch. Inside a graph the reduce starts as the split
+        # kernel ends, but every replay costs several µs before its first
+        # kernel. A model's decode graph holds one attention step per layer,
+        # so that cost is shared by all of them: the K timed steps are
+        # captured back to back in one graph and replayed once (exactly K
+        # steps). Workloads that flush the MALL before every step replay a
+        # one-step graph per step instead (the flush sits between replays).
+        # The one-step-per-replay rate is reported beside it.
+        def capture(n: int) -> torch.cuda.CUDAGraph:
+            side = torch.cuda.Stream(device)
+            side.wait_stream(torch.cuda.current_stream(device))
+            with torch.cuda.stream(side):
+                run_step()
+            torch.cuda.current_stream(device).wait_stream(side)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(n):
+                    run_step()
+            return g
+
+        one = capture(1)
         for _ in range(warmup):
-            graph.replay()
+            one.replay()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for i in range(k_steps):
             flush_mall(i)
-            graph.replay()
+            one.replay()
         torch.cuda.synchronize()
-        wall_s = time.perf_counter() - t0 - flush_seconds()
-        step_mode = "hip graph replay"
+        single_s = time.perf_counter() - t0 - flush_seconds()
+        single_graph_us = single_s * 1e6 / k_steps
+        wall_s = single_s
+        step_mode = "hip graph replay, one step per replay"
+        if flush_buf is None:
+            many = capture(k_steps)
+            many.replay()  # warm
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            many.replay()
+            torch.cuda.synchronize()
+            wall_s = time.perf_counter() - t0
+            step_mode = "hip graph of the K steps back to back, replayed once"
+            del many
     torch.cuda.synchronize()
     # every timed step recomputes the checked output (same inputs; the
     # append writes past each context): the last one must equal it bit for bit
@@ -764,6 +799,7 @@ def main() -> int:
                         "event-timed 512 MiB MALL flush written before each step" if flush
                         else "wall clock around the K steps, synchronized on both sides"),
         "eager_us_per_step": round(eager_wall_s * 1e6 / k_steps, 1),
+        "one_step_graph_us_per_step": round(single_graph_us, 1) if single_graph_us is not None else None,
         "pct_of_peak_hbm": round(100 * step_gbps / PEAK_HBM_GBPS, 1),
         "higher_is_better": True,
         "scaling": "weak",
@@ -784,11 +820,16 @@ def main() -> int:
             "partition_size": attn.partition_size,
             "split": "balanced (equal tile runs per resident wave)" if attn.balanced_split
                      else f"fixed partitions of {attn.partition_size} tokens",
-            "step": "paged attention (split kernel + reduce) then 1-token KV append per request",
+            "step": ("paged attention (split kernel + reduce) then 1-token KV append per request: "
+                     + ("two operator launches" if args.separate_append or not step.fused
+                        else "one library call, the append carried by the reduce kernel")),
+            "kernels": ([n for n in attn.kernel_names() if n] + ["append_kv_kernel"] if args.separate_append
+                        else list(step.kernel_names())),
             "parallelism": "single GPU",
         },
         "attention_kernel_us": round(kern_avg_ms * 1e3, 2),
         "reduce_kernel_us": round(sum(reduce_ms) / len(reduce_ms) * 1e3, 2),
+        "reduce_carries_append": bool(step.fused and not args.separate_append),
         "algorithmic_bytes_per_step": attn_bytes + append_bytes,
         "roofline": {
             "bound": "hbm",

@@ -292,6 +292,27 @@ int32_t ikl_paged_attention_partition_size(const ikl_paged_attention_args *args)
  * kernels never read outside the cache. Replaces triton_ops.py:404-610. */
 int ikl_paged_attention(const ikl_paged_attention_args *args, void *stream);
 
+/* One decode step of the synthetic runner's order (decode.py:480-487):
+ * paged decode attention over context_lens, then the KV append of the
+ * step's new rows. When the attention splits (a reduce kernel runs) and the
+ * append is a plain copy in 16-byte pieces (16-bit or fp32 cache, aligned
+ * rows of at most 512 bytes), the reduce kernel's workgroups also do the
+ * append: one launch less per step, with the same result as
+ * ikl_paged_attention followed by ikl_append_kv (the reduce runs after the
+ * attention kernel has read the cache). Otherwise the two run as separate
+ * launches in that order. Both argument structs are validated before
+ * anything is enqueued, except an FP8 append's own checks, which run after
+ * the attention has been enqueued. No counterpart in the reference, which
+ * launches the two operators separately. */
+int ikl_paged_decode_step(const ikl_paged_attention_args *attention, const ikl_append_args *append,
+                          void *stream);
+
+/* 1 when ikl_paged_decode_step with these arguments fuses the append into
+ * the reduce kernel, 0 when it launches it separately, negative on invalid
+ * arguments. Planning only: launches nothing. */
+int32_t ikl_paged_decode_step_fused(const ikl_paged_attention_args *attention,
+                                    const ikl_append_args *append);
+
 /* Static path selection for a grouped launch; mirrors the role of
  * paged_decode_grouped_path (triton_ops.py:56-75) for this library's
  * kernel families: MHA (heads_per_kv == 1) -> IKL_PATH_MHA_FALLBACK;

@@ -21,8 +21,12 @@ from .ops import (
     paged_decode_grouped_autotune_config,
     paged_decode_grouped_dot_autotune_config,
     paged_decode_grouped_path,
+    paged_decode_step_hip,
     paged_prefill_attention_hip,
     paged_prefill_path,
+    PreparedAppend,
+    PreparedDecodeStep,
+    PreparedPagedAttention,
     PreparedPagedPrefill,
     rope_append_kv_hip,
     triton_append_available,
@@ -49,6 +53,10 @@ __all__ = [
     "paged_decode_attention_triton",
     "paged_decode_attention_triton_grouped",
     "paged_decode_grouped_path",
+    "paged_decode_step_hip",
+    "PreparedAppend",
+    "PreparedDecodeStep",
+    "PreparedPagedAttention",
     "paged_prefill_attention_hip",
     "paged_prefill_path",
     "PreparedPagedPrefill",

@@ -35,6 +35,8 @@ EXPORTED_SYMBOLS = (
     "ikl_rope_append_kv",
     "ikl_paged_prefill_attention",
     "ikl_paged_prefill_path",
+    "ikl_paged_decode_step",
+    "ikl_paged_decode_step_fused",
 )
 
 _c_i64 = ctypes.c_int64
@@ -255,6 +257,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ikl_paged_prefill_attention.argtypes = [ctypes.POINTER(PagedPrefillArgs), _c_ptr]
     lib.ikl_paged_prefill_path.restype = _c_i32
     lib.ikl_paged_prefill_path.argtypes = [_c_i32, _c_i32, _c_i32]
+    lib.ikl_paged_decode_step.restype = ctypes.c_int
+    lib.ikl_paged_decode_step.argtypes = [ctypes.POINTER(PagedAttentionArgs), ctypes.POINTER(AppendArgs), _c_ptr]
+    lib.ikl_paged_decode_step_fused.restype = _c_i32
+    lib.ikl_paged_decode_step_fused.argtypes = [ctypes.POINTER(PagedAttentionArgs), ctypes.POINTER(AppendArgs)]
     lib.ikl_paged_attention_launch_config.restype = ctypes.c_int
     lib.ikl_paged_attention_launch_config.argtypes = [ctypes.POINTER(PagedAttentionArgs),
                                                       ctypes.POINTER(LaunchConfig)]

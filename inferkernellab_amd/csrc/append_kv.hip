@@ -10,6 +10,7 @@
 // program. Slots outside the cache are skipped (the reference's Triton
 // kernel has no bound check, append.py:44-66).
 #include "ikl_common.h"
+#include "paged_attn.h"
 
 namespace ikl {
 namespace {
@@ -231,20 +232,29 @@ int append_fp8(const ikl_append_args *a, hipStream_t s) {
 
 using namespace ikl;
 
-extern "C" int ikl_append_kv(const ikl_append_args *a, void *stream) {
+namespace ikl {
+namespace {
+
+// Checks shared by ikl_append_kv and the fused append of a decode step.
+int check_append(const ikl_append_args *a) {
   if (!a) return fail(IKL_EINVAL, "append: null argument struct");
   if (a->num_tokens < 0) return fail(IKL_EINVAL, "append: num_tokens must be non-negative");
-  if (a->num_tokens == 0) return IKL_OK;
   if (a->num_tokens > 0x7fffffffLL) return fail(IKL_EINVAL, "append: too many tokens for one launch");
+  if (a->num_tokens == 0) return IKL_OK;
   if (a->block_size <= 0 || a->num_blocks <= 0 || a->num_kv_heads <= 0 || a->head_dim <= 0)
     return fail(IKL_EINVAL, "append: cache dimensions must be positive");
   if (!a->key || !a->value || !a->slots || !a->k_cache || !a->v_cache)
     return fail(IKL_EINVAL, "append: null tensor pointer");
   if (a->slot_type != IKL_I32 && a->slot_type != IKL_I64)
     return fail(IKL_EINVAL, "append: slots must use int32 or int64");
-  if (a->cache_dtype == IKL_FP8_E4M3) return append_fp8(a, (hipStream_t)stream);
-  if (a->cache_dtype != 0 && a->cache_dtype != a->dtype)
+  if (a->cache_dtype != 0 && a->cache_dtype != a->dtype && a->cache_dtype != IKL_FP8_E4M3)
     return fail(IKL_EINVAL, "append: cache_dtype must be 0, the key dtype or IKL_FP8_E4M3");
+  return IKL_OK;
+}
+
+// Byte-stride parameters of a plain-copy append and the widest chunk (16, 4
+// or the element size) that every row start and the row length allow.
+int copy_params(const ikl_append_args *a, AppendParams &p, int &chunk) {
   int eb;
   switch (a->dtype) {
     case IKL_F16:
@@ -252,7 +262,6 @@ extern "C" int ikl_append_kv(const ikl_append_args *a, void *stream) {
     case IKL_F32: eb = 4; break;
     default: return fail(IKL_EINVAL, "append: unsupported dtype");
   }
-  AppendParams p;
   p.key = (const char *)a->key;
   p.value = (const char *)a->value;
   p.key_st = a->key_stride_t * eb;
@@ -271,18 +280,67 @@ extern "C" int ikl_append_kv(const ikl_append_args *a, void *stream) {
   p.num_slots = a->num_blocks * (int64_t)a->block_size;
   p.block_size = a->block_size;
   p.num_kv_heads = a->num_kv_heads;
-
   const int64_t row_bytes = (int64_t)a->head_dim * eb;
-  // Widest chunk that every row start and the row length allow.
   auto fits = [&](int64_t n) {
     return row_bytes % n == 0 && p.key_st % n == 0 && p.key_sh % n == 0 && p.value_st % n == 0 &&
            p.value_sh % n == 0 && p.kc_sb % n == 0 && p.kc_st % n == 0 && p.kc_sh % n == 0 &&
            p.vc_sb % n == 0 && p.vc_st % n == 0 && p.vc_sh % n == 0 && aligned(a->key, n) &&
            aligned(a->value, n) && aligned(a->k_cache, n) && aligned(a->v_cache, n);
   };
-  int chunk = fits(16) ? 16 : fits(4) ? 4 : eb;
+  chunk = fits(16) ? 16 : fits(4) ? 4 : eb;
   if (!fits(chunk)) return fail(IKL_EINVAL, "append: tensors are not element aligned");
   p.chunks_per_head = (int32_t)(row_bytes / chunk);
+  return IKL_OK;
+}
+
+}  // namespace
+
+int prepare_fused_append(const ikl_append_args *a, FusedAppend &f) {
+  f = FusedAppend{};
+  const int rc = check_append(a);
+  if (rc != IKL_OK || a->num_tokens == 0) return rc;
+  if (a->cache_dtype == IKL_FP8_E4M3) return 1;
+  AppendParams p;
+  int chunk = 0;
+  const int prc = copy_params(a, p, chunk);
+  if (prc != IKL_OK) return prc;
+  if (chunk != 16 || p.chunks_per_head > 32) return 1;
+  f.key = p.key;
+  f.value = p.value;
+  f.key_st = p.key_st;
+  f.key_sh = p.key_sh;
+  f.value_st = p.value_st;
+  f.value_sh = p.value_sh;
+  f.slots = p.slots;
+  f.kc = p.kc;
+  f.vc = p.vc;
+  f.kc_sb = p.kc_sb;
+  f.kc_st = p.kc_st;
+  f.kc_sh = p.kc_sh;
+  f.vc_sb = p.vc_sb;
+  f.vc_st = p.vc_st;
+  f.vc_sh = p.vc_sh;
+  f.rows = a->num_tokens * (int64_t)a->num_kv_heads;
+  f.num_slots = p.num_slots;
+  f.kv_heads = a->num_kv_heads;
+  f.chunks = p.chunks_per_head;
+  f.block_size = a->block_size;
+  f.slots_i64 = a->slot_type == IKL_I64;
+  return IKL_OK;
+}
+
+}  // namespace ikl
+
+using namespace ikl;
+
+extern "C" int ikl_append_kv(const ikl_append_args *a, void *stream) {
+  const int rc = check_append(a);
+  if (rc != IKL_OK || a->num_tokens == 0) return rc;
+  if (a->cache_dtype == IKL_FP8_E4M3) return append_fp8(a, (hipStream_t)stream);
+  AppendParams p;
+  int chunk = 0;
+  const int prc = copy_params(a, p, chunk);
+  if (prc != IKL_OK) return prc;
   const int total = a->num_kv_heads * p.chunks_per_head;
   int threads = total >= 256 ? 256 : ((total + 63) / 64) * 64;
   dim3 grid((unsigned)a->num_tokens);

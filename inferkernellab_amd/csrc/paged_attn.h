@@ -14,6 +14,32 @@ constexpr float LOG2E = 1.4426950408889634f;
 constexpr float NEG_SENTINEL = -1.0e30f;  // finite "minus infinity" for running maxima
 constexpr float RESCALE_LOG2 = 8.0f;      // lazy-rescale threshold (factor 256)
 
+// KV append carried by the split reduce kernel (ikl_paged_decode_step): its
+// workgroups also scatter `rows` (token, kv head) rows of new K/V into the
+// cache, as ikl_append_kv does. Only for plain copies in 16-byte chunks
+// (16-bit or fp32 caches, aligned rows of at most 32 chunks).
+struct FusedAppend {
+  const char *key;
+  const char *value;
+  int64_t key_st, key_sh, value_st, value_sh;  // bytes
+  const void *slots;
+  char *kc;
+  char *vc;
+  int64_t kc_sb, kc_st, kc_sh, vc_sb, vc_st, vc_sh;  // bytes
+  int64_t rows;       // tokens x kv heads; 0 = nothing to append
+  int64_t num_slots;  // num_blocks * block_size
+  int32_t kv_heads;
+  int32_t chunks;     // 16-byte chunks per head row, <= 32
+  int32_t block_size;
+  int32_t slots_i64;
+};
+
+// Fills `f` from the arguments of an ikl_append_kv call: IKL_OK when the
+// append can ride on the reduce kernel, 1 when it is valid but must run as
+// its own launch (FP8 cache, rows not 16-byte aligned or longer than 512
+// bytes), an IKL_E* code when the arguments are invalid (message set).
+int prepare_fused_append(const ikl_append_args *a, FusedAppend &f);
+
 struct AttnParams {
   const char *q;
   int64_t q_sb, q_sh;  // elements
@@ -59,6 +85,7 @@ struct AttnParams {
   const float *k_scale;
   const float *v_scale;
   int64_t s_sb, s_sh;      // elements
+  FusedAppend app;         // rows == 0 unless a decode step fuses its append
 };
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

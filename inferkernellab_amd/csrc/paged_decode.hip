@@ -304,6 +304,44 @@ __global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParam
   }
 }
 
+// Fused KV append of a decode step: the reduce workgroups, flattened to
+// wg in [0, nwg), take rows (token t, kv head h) of the new K/V; a pass
+// covers R = 64 / (2 chunks) rows per workgroup, and lane l copies K chunk
+// l % (2 chunks) (V chunk when >= chunks) of row wg R + l / (2 chunks). The
+// loads are issued when the kernel starts and the stores placed after the
+// partials are read, so the copy's round trip overlaps the reduce's.
+struct FusedRow {
+  v4u32 data;
+  int64_t slot, t;
+  int h, c;
+  bool on, is_v;
+};
+
+__device__ inline FusedRow fused_append_load(const FusedAppend &f, int64_t row0, int lane) {
+  FusedRow r{};
+  const int per_row = 2 * f.chunks;
+  const int sub = lane % per_row;
+  const int64_t row = row0 + lane / per_row;
+  r.on = lane / per_row < 64 / per_row && row < f.rows;
+  if (!r.on) return r;
+  r.is_v = sub >= f.chunks;
+  r.c = r.is_v ? sub - f.chunks : sub;
+  r.t = row / f.kv_heads;
+  r.h = (int)(row - r.t * f.kv_heads);
+  r.slot = f.slots_i64 ? load_index<int64_t>(f.slots, r.t) : load_index<int32_t>(f.slots, r.t);
+  const char *src = r.is_v ? f.value + r.t * f.value_st + r.h * f.value_sh : f.key + r.t * f.key_st + r.h * f.key_sh;
+  r.data = load16v_global(src + r.c * 16);
+  return r;
+}
+
+__device__ inline void fused_append_store(const FusedAppend &f, const FusedRow &r) {
+  if (!r.on || r.slot < 0 || r.slot >= f.num_slots) return;  // slots outside the cache are skipped
+  const int64_t blk = r.slot / f.block_size, off = r.slot - blk * f.block_size;
+  char *dst = r.is_v ? f.vc + blk * f.vc_sb + off * f.vc_st + r.h * f.vc_sh
+                     : f.kc + blk * f.kc_sb + off * f.kc_st + r.h * f.kc_sh;
+  *reinterpret_cast<v4u32 *>(dst + r.c * 16) = r.data;
+}
+
 // Combines the split partials of one (request, head):
 //   out = sum_p 2^(lse_p - M) o_p / sum_p 2^(lse_p - M),  M = max_p lse_p.
 // Lanes split into GROUPS groups of D/4 lanes; group j takes partitions
@@ -320,6 +358,10 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(const AttnParam
   const int lane = threadIdx.x;
   const int64_t hq = blockIdx.x;
   const int64_t b = blockIdx.y;
+  // fused append: first pass loaded now, stored once the partials are in
+  const int64_t wg = b * gridDim.x + hq, nwg = (int64_t)gridDim.x * gridDim.y;
+  const int64_t app_rpp = p.app.rows > 0 ? 64 / (2 * p.app.chunks) : 0;
+  const FusedRow first_row = p.app.rows > 0 ? fused_append_load(p.app, wg * app_rpp, lane) : FusedRow{};
   int np;
   int64_t prow, pstride;
   if (p.sk_waves > 0) {
@@ -373,6 +415,11 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(const AttnParam
       part_z[grp] = z;
       part_m[grp] = m;
     }
+  }
+  if (p.app.rows > 0) {
+    fused_append_store(p.app, first_row);
+    for (int64_t row0 = (wg + nwg) * app_rpp; row0 < p.app.rows; row0 += nwg * app_rpp)
+      fused_append_store(p.app, fused_append_load(p.app, row0, lane));
   }
   __syncthreads();
   if (lane >= CH) return;
@@ -720,10 +767,11 @@ extern "C" int32_t ikl_paged_attention_path(int32_t dtype, int32_t head_dim, int
   return select_path(dtype, head_dim, block_size, heads_per_kv, query_group_size);
 }
 
-extern "C" int ikl_paged_attention(const ikl_paged_attention_args *a, void *stream) {
-  Plan pl;
-  int rc = make_plan(a, pl);
-  if (rc != IKL_OK) return rc;
+namespace ikl {
+namespace {
+// Validates and enqueues one attention launch; `app` (optional) rides on the
+// split reduce kernel, which the caller has checked runs (pl.split).
+int run_attention(const ikl_paged_attention_args *a, const Plan &pl, const FusedAppend *app, void *stream) {
   if (!a->query || !a->k_cache || !a->v_cache || !a->block_tables || !a->context_lens || !a->out)
     return fail(IKL_EINVAL, "attention: null tensor pointer");
   const int vec = 16 / pl.eb;
@@ -793,6 +841,7 @@ extern "C" int ikl_paged_attention(const ikl_paged_attention_args *a, void *stre
   p.v_scale = (const float *)a->v_scale;
   p.s_sb = a->scale_stride_block;
   p.s_sh = a->scale_stride_head;
+  p.app = app ? *app : FusedAppend{};
 
   dim3 grid((unsigned)pl.num_parts, (unsigned)(a->num_kv_heads * pl.groups_per_kv), (unsigned)a->batch);
   hipStream_t s = (hipStream_t)stream;
@@ -814,4 +863,40 @@ extern "C" int ikl_paged_attention(const ikl_paged_attention_args *a, void *stre
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(IKL_ELAUNCH, std::string("paged attention launch: ") + hipGetErrorString(e));
   return IKL_OK;
+}
+
+// Whether a decode step's append rides on the reduce kernel (1), runs as
+// its own launch after the attention (0), or the arguments are invalid (<0).
+int step_plan(const ikl_paged_attention_args *a, const ikl_append_args *app, Plan &pl, FusedAppend &f) {
+  int rc = make_plan(a, pl);
+  if (rc != IKL_OK) return rc;
+  rc = prepare_fused_append(app, f);
+  if (rc < 0) return rc;
+  return rc == IKL_OK && f.rows > 0 && pl.split ? 1 : 0;
+}
+}  // namespace
+}  // namespace ikl
+
+extern "C" int ikl_paged_attention(const ikl_paged_attention_args *a, void *stream) {
+  Plan pl;
+  const int rc = make_plan(a, pl);
+  if (rc != IKL_OK) return rc;
+  return run_attention(a, pl, nullptr, stream);
+}
+
+extern "C" int32_t ikl_paged_decode_step_fused(const ikl_paged_attention_args *a, const ikl_append_args *app) {
+  Plan pl;
+  FusedAppend f;
+  return step_plan(a, app, pl, f);
+}
+
+extern "C" int ikl_paged_decode_step(const ikl_paged_attention_args *a, const ikl_append_args *app,
+                                     void *stream) {
+  Plan pl;
+  FusedAppend f;
+  const int mode = step_plan(a, app, pl, f);
+  if (mode < 0) return mode;
+  const int rc = run_attention(a, pl, mode == 1 ? &f : nullptr, stream);
+  if (rc != IKL_OK || mode == 1 || app->num_tokens == 0) return rc;
+  return ikl_append_kv(app, stream);
 }

@@ -661,6 +661,68 @@ class PreparedAppend:
         _lib.check(status, "append_kv")
 
 
+class PreparedDecodeStep:
+    """One decode step on bound buffers: paged decode attention of
+    ``attention`` (a :class:`PreparedPagedAttention`), then the KV append of
+    ``append`` (a :class:`PreparedAppend`), in the synthetic runner's order
+    (decode.py:480-487), enqueued by one library call
+    (``ikl_paged_decode_step``). When the attention splits, the reduce
+    kernel also carries the append — one launch less per step — with the
+    same result as calling the two separately (``fused`` tells which)."""
+
+    def __init__(self, attention: PreparedPagedAttention, append: PreparedAppend):
+        if attention.device != append.device:
+            raise ValueError("attention and append must be on the same device")
+        self._lib = _require_backend()
+        self.attention, self.append = attention, append
+        mode = self._lib.ikl_paged_decode_step_fused(ctypes.byref(attention._args), ctypes.byref(append._args))
+        _lib.check(mode if mode < 0 else 0, "decode step")
+        self.fused = mode == 1
+        self.device = attention.device
+
+    @property
+    def out(self) -> torch.Tensor:
+        return self.attention.out
+
+    def kernel_names(self) -> tuple[str, ...]:
+        """Kernels one step enqueues, in order."""
+        names = tuple(n for n in self.attention.kernel_names() if n)
+        return names if self.fused else names + ("append_kv_kernel",)
+
+    def __call__(self, events=None) -> torch.Tensor:
+        a = self.attention._args
+        for i in range(3):
+            a.events[i] = events[i] if events is not None else None
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        status = self._lib.ikl_paged_decode_step(ctypes.byref(a), ctypes.byref(self.append._args),
+                                                 ctypes.c_void_p(stream))
+        _lib.check(status, "decode step")
+        return self.attention.out
+
+
+def paged_decode_step_hip(query, cache, block_tables, context_lens, key, value, slots, scale=None, layer=0, *,
+                          validate_inputs=True, partition_size: int | None = None,
+                          max_context_len: int | None = None) -> torch.Tensor:
+    """Attention of ``query`` over the paged contexts, then the append of
+    ``key`` / ``value`` rows ``[T, Hkv, D]`` at ``slots`` (same checks as
+    :func:`paged_decode_attention_hip` and :func:`append_kv_hip`); returns the
+    attention output. One library call; see :class:`PreparedDecodeStep`."""
+    if key.stride(-1) != 1:
+        key = key.contiguous()
+    if value.stride(-1) != 1:
+        value = value.contiguous()
+    slots = slots.reshape(-1)
+    if slots.numel() and slots.stride(0) != 1:
+        slots = slots.contiguous()
+    if not _aligned_rows(query):
+        query = query.contiguous()
+    attention = PreparedPagedAttention(query, cache, block_tables, context_lens, scale, layer,
+                                       partition_size=partition_size, max_context_len=max_context_len,
+                                       validate_inputs=validate_inputs)
+    append = PreparedAppend(key, value, cache, slots, layer)
+    return PreparedDecodeStep(attention, append)()
+
+
 # ------------------------------------------------------------ prefill
 def paged_prefill_path(*, dtype: torch.dtype, head_dim: int, block_size: int = 16) -> str:
     """Kernel family of a prefill launch: ``"mfma_grouped"`` for fp16/bf16

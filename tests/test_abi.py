@@ -385,3 +385,37 @@ def test_prefill_operator_checks_in_the_reference_order(shape, tables, starts, e
     q = torch.zeros(shape, dtype=torch.bfloat16)
     with pytest.raises(error, match=message):
         ops.paged_prefill_attention_hip(q, cache, tables, starts, ends, layer=layer)
+
+
+def _append_args(**kw):
+    a = _lib.AppendArgs()
+    a.key, a.value, a.slots, a.k_cache, a.v_cache = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000
+    a.key_stride_t, a.key_stride_h = 8 * 128, 128
+    a.value_stride_t, a.value_stride_h = 8 * 128, 128
+    a.k_stride_block, a.k_stride_token, a.k_stride_head = 16 * 8 * 128, 8 * 128, 128
+    a.v_stride_block, a.v_stride_token, a.v_stride_head = 16 * 8 * 128, 8 * 128, 128
+    a.num_tokens, a.num_blocks, a.block_size, a.num_kv_heads, a.head_dim = 32, 20000, 16, 8, 128
+    a.slot_type, a.dtype = _lib.IKL_I32, _lib.IKL_BF16
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "attn_kw,append_kw,expect",
+    [
+        ({}, {}, 1),                                   # balanced split + 16-byte rows: fused
+        ({"partition_size": 512}, {}, 1),              # fixed partitions split too
+        ({"partition_size": -1}, {}, 0),               # no reduce kernel: separate append
+        ({}, {"cache_dtype": _lib.IKL_FP8_E4M3}, 0),   # FP8 append quantises: separate
+        ({}, {"key": 0x10008}, 0),                     # rows only 8-byte aligned: separate
+        ({}, {"num_tokens": 0}, 0),                    # nothing to append
+        ({}, {"key": 0}, _lib.IKL_EINVAL),             # invalid append
+        ({"num_heads": 7}, {}, _lib.IKL_EINVAL),       # invalid attention
+    ],
+)
+def test_decode_step_fuses_the_append_into_the_reduce(attn_kw, append_kw, expect):
+    """ikl_paged_decode_step_fused: planning only, no GPU."""
+    lib = _lib.load()
+    a = _args(max_context_len=8192, **attn_kw)
+    assert lib.ikl_paged_decode_step_fused(ctypes.byref(a), ctypes.byref(_append_args(**append_kw))) == expect
