@@ -373,7 +373,7 @@ class SyntheticDecodeRunner:
         prefill_steps, prefill_dev, decode_wall, decode_dev = [], 0.0, [], []
         peak_blocks = self.cache.allocator.num_used_blocks
         try:
-            with torch.inference_mode():
+            with torch.no_grad():  # no inference tensors: callers may capture graphs later
                 while self.runtime.scheduler.waiting or self.runtime.scheduler.running:
                     batch, wall_ms, dev_ms = self._timed_step()
                     peak_blocks = max(peak_blocks, self.cache.allocator.num_used_blocks)

@@ -562,7 +562,11 @@ class LlamaPagedDecodeRunner:
         torch.cuda.reset_peak_memory_stats(self.device)
         prefill_steps, decode_steps = [], []
         peak_blocks = self.cache.allocator.num_used_blocks
-        with torch.inference_mode():
+        # no_grad, not inference_mode: the decode graph captured below would
+        # otherwise create torch's graph-safe generator state as inference
+        # tensors, and any later capture in the process outside inference
+        # mode would fail on it
+        with torch.no_grad():
             while self.runtime.scheduler.waiting or self.runtime.scheduler.running:
                 t0 = time.perf_counter()
                 batch = self.runtime.step()
