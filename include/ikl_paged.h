@@ -292,6 +292,22 @@ int32_t ikl_paged_attention_partition_size(const ikl_paged_attention_args *args)
  * kernels never read outside the cache. Replaces triton_ops.py:404-610. */
 int ikl_paged_attention(const ikl_paged_attention_args *args, void *stream);
 
+/* Bytes of the per-device scratch array behind ikl_paged_attention_noalloc. */
+#define IKL_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* ikl_paged_attention without a caller workspace and without any device
+ * allocation: the split partials go to a 16 MiB array the library holds on
+ * each device for the life of the process (found once per device with
+ * hipGetSymbolAddress, on the first call with that device current). No
+ * counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). args->workspace / workspace_bytes are ignored. A launch whose
+ * split needs more than IKL_NOALLOC_SCRATCH_BYTES (see
+ * ikl_paged_attention_workspace_size) fails with IKL_EWORKSPACE. All calls
+ * on one device share the array: calls that overlap on that device (on
+ * different streams, or concurrently from several threads) race. */
+int ikl_paged_attention_noalloc(const ikl_paged_attention_args *args, void *stream);
+
 /* One decode step of the synthetic runner's order (decode.py:480-487):
  * paged decode attention over context_lens, then the KV append of the
  * step's new rows. When the attention splits (a reduce kernel runs) and the

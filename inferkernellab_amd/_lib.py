@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "ikl_paged_prefill_path",
     "ikl_paged_decode_step",
     "ikl_paged_decode_step_fused",
+    "ikl_paged_attention_noalloc",
 )
 
 _c_i64 = ctypes.c_int64
@@ -257,6 +258,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ikl_paged_prefill_attention.argtypes = [ctypes.POINTER(PagedPrefillArgs), _c_ptr]
     lib.ikl_paged_prefill_path.restype = _c_i32
     lib.ikl_paged_prefill_path.argtypes = [_c_i32, _c_i32, _c_i32]
+    lib.ikl_paged_attention_noalloc.restype = ctypes.c_int
+    lib.ikl_paged_attention_noalloc.argtypes = [ctypes.POINTER(PagedAttentionArgs), _c_ptr]
     lib.ikl_paged_decode_step.restype = ctypes.c_int
     lib.ikl_paged_decode_step.argtypes = [ctypes.POINTER(PagedAttentionArgs), ctypes.POINTER(AppendArgs), _c_ptr]
     lib.ikl_paged_decode_step_fused.restype = _c_i32

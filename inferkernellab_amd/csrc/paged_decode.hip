@@ -27,6 +27,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "ikl_common.h"
@@ -882,6 +883,66 @@ extern "C" int ikl_paged_attention(const ikl_paged_attention_args *a, void *stre
   const int rc = make_plan(a, pl);
   if (rc != IKL_OK) return rc;
   return run_attention(a, pl, nullptr, stream);
+}
+
+// Split workspace of ikl_paged_attention_noalloc: one array per device for
+// the whole process. Every call on a device shares it, so calls that
+// overlap on one device race; nothing in it needs clearing (each launch
+// writes every partial its reduce reads).
+static __device__ __align__(256) unsigned char scratch[IKL_NOALLOC_SCRATCH_BYTES];
+
+namespace ikl {
+namespace {
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[SCRATCH_MAX_DEVICES] = {};
+
+// Device address of `scratch` on the current device, looked up once per
+// device (the array's name is only a host-side stand-in).
+int scratch_address(void **out) {
+  int dev = -1;
+  const hipError_t de = hipGetDevice(&dev);
+  if (de != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(IKL_ELAUNCH, std::string("attention (no-alloc): no current device: ") + hipGetErrorString(de));
+  }
+  if (dev < 0 || dev >= SCRATCH_MAX_DEVICES)
+    return fail(IKL_EUNSUPPORTED, "attention (no-alloc): device index beyond 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      return fail(IKL_ELAUNCH, std::string("attention (no-alloc): hipGetSymbolAddress(scratch) failed: ") +
+                                   hipGetErrorString(e));
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return IKL_OK;
+}
+}  // namespace
+}  // namespace ikl
+
+extern "C" int ikl_paged_attention_noalloc(const ikl_paged_attention_args *a, void *stream) {
+  Plan pl;
+  int rc = make_plan(a, pl);
+  if (rc != IKL_OK) return rc;
+  if (pl.ws_bytes > (int64_t)IKL_NOALLOC_SCRATCH_BYTES)
+    return fail(IKL_EWORKSPACE, "attention (no-alloc): the launch needs " + std::to_string(pl.ws_bytes) +
+                                    " bytes of split workspace, more than the " +
+                                    std::to_string((int64_t)IKL_NOALLOC_SCRATCH_BYTES) +
+                                    "-byte scratch; call ikl_paged_attention with a workspace instead");
+  ikl_paged_attention_args b = *a;
+  b.workspace = nullptr;
+  b.workspace_bytes = 0;
+  if (pl.split) {
+    rc = scratch_address(&b.workspace);
+    if (rc != IKL_OK) return rc;
+    b.workspace_bytes = (int64_t)IKL_NOALLOC_SCRATCH_BYTES;
+  }
+  return run_attention(&b, pl, nullptr, stream);
 }
 
 extern "C" int32_t ikl_paged_decode_step_fused(const ikl_paged_attention_args *a, const ikl_append_args *app) {

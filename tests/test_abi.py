@@ -419,3 +419,13 @@ def test_decode_step_fuses_the_append_into_the_reduce(attn_kw, append_kw, expect
     lib = _lib.load()
     a = _args(max_context_len=8192, **attn_kw)
     assert lib.ikl_paged_decode_step_fused(ctypes.byref(a), ctypes.byref(_append_args(**append_kw))) == expect
+
+
+def test_noalloc_rejects_a_split_beyond_its_scratch_without_a_gpu():
+    """A launch whose split workspace exceeds the 16 MiB scratch is refused
+    before anything is touched or enqueued."""
+    lib = _lib.load()
+    a = _args(batch=64, partition_size=64, max_context_len=8192, table_width=512)
+    assert lib.ikl_paged_attention_workspace_size(ctypes.byref(a)) > (16 << 20)
+    assert lib.ikl_paged_attention_noalloc(ctypes.byref(a), None) == _lib.IKL_EWORKSPACE
+    assert "scratch" in _lib.last_error()
