@@ -790,6 +790,13 @@ int run_attention(const ikl_paged_attention_args *a, const Plan &pl, const Fused
        16 * a->v_stride_token * (pl.kv_fp8 ? 1 : pl.eb) >= (int64_t(1) << 31) ||
        a->k_stride_token < a->head_dim || a->v_stride_token < a->head_dim))
     return fail(IKL_EINVAL, "attention: token strides must lie in [head_dim, 2^27 bytes / 16)");
+  // ... and reaches a tile's block through a 32-bit block stride in bytes
+  if (pl.path == IKL_PATH_MFMA_GROUPED &&
+      (a->k_stride_block * (pl.kv_fp8 ? 1 : pl.eb) >= (int64_t(1) << 32) ||
+       a->v_stride_block * (pl.kv_fp8 ? 1 : pl.eb) >= (int64_t(1) << 32) || a->k_stride_block < 0 ||
+       a->v_stride_block < 0 || (pl.kv_fp8 && (a->scale_stride_block * 4 >= (int64_t(1) << 32) ||
+                                                a->scale_stride_head * 4 >= (int64_t(1) << 31)))))
+    return fail(IKL_EINVAL, "attention: block strides must lie below 4 GiB");
   if (pl.kv_fp8 && (!a->k_scale || !a->v_scale || !aligned16(a->k_scale) || !aligned16(a->v_scale) ||
                     a->scale_stride_block % 4 || a->scale_stride_head % 4))
     return fail(IKL_EINVAL, "attention: the FP8 cache needs 16-byte aligned k_scale / v_scale rows");

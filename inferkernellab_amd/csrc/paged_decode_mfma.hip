@@ -27,6 +27,8 @@
 //    wave starts once, streams ~T/W tiles and all finish together.
 //
 // MFMA operand layouts and the transposing LDS read: see mfma_ops.h.
+#include <type_traits>
+
 #include "ikl_common.h"
 #include "mfma_ops.h"
 #include "paged_attn.h"
@@ -35,13 +37,16 @@ namespace ikl {
 namespace {
 
 constexpr int TILE = 16;  // tokens per tile
+constexpr int CPOL_NT = 2;  // buffer-load cache policy: non-temporal (K/V rows are read once)
 
 // Register budget: the FP8 kernels with 16-head units ask for at least 2
 // waves per SIMD (VGPRs + AGPRs <= 256): they then keep their accumulators
 // in VGPRs, without the accumulator-register copies the compiler otherwise
 // places in every tile (81 -> 78 us on the FP8 GQA decode workload). The
 // others keep the compiler's choice (the 32-head kernels would spill; the
-// 16-bit 16-head one measured no better).
+// 16-bit 16-head ones fit two waves anyway). Two waves per SIMD for the
+// fixed-partition 32-head kernel (217 VGPRs without the split masking
+// path) measured slower on MQA: 31.0 against 28.4 us.
 #define IKL_MFMA_WAVES_ATTR __attribute__((amdgpu_waves_per_eu(KV8 && NG == 1 ? 2 : 1, 8)))
 
 // bf16 P enters the PV product with its rounding residual in a second MFMA
@@ -107,7 +112,6 @@ struct WaveTiles {
   static constexpr int ST_BYTES = NH * SROW * 4;            // one staged [NH heads x D] block
   using ops = mfma_ops<Tag>;
   typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-  typedef const __attribute__((address_space(1))) u32x2v *global_u32x2_ptr;
 
   struct Tile {
     v4u32 k[KSTEPS];       // 16-bit: one operand per k-step; KV8: raw codes, 8 bytes per k-step
@@ -130,7 +134,7 @@ struct WaveTiles {
     lane = threadIdx.x & 63;
     hl = lane & 15;   // MFMA row/column index inside a 16-lane group
     grp = lane >> 4;  // 16-lane group
-    k_lane = (hl * (int)p.k_st + k_elem(0)) * CEB;  // token hl, first element of k-step 0
+    k_lane = hl * (int)p.k_st * CEB + k_elem(0) * CEB;  // token hl, first element of k-step 0 (bytes)
 #pragma unroll
     for (int u = 0; u < VLOADS; ++u) {
       // V cache piece: row pi / CPIECES, piece pi % CPIECES; for KV8 it widens
@@ -178,13 +182,17 @@ struct WaveTiles {
     const int n_tiles = t1 > t0 ? (int)((t1 - t0 + TILE - 1) / TILE) : 0;
     const char *kbase = p.kc + (int64_t)kvh * p.k_sh * CEB;
     const char *vbase = p.vc + (int64_t)kvh * p.v_sh * CEB;
-    const char *zero_row = reinterpret_cast<const char *>(g_zero_row);
+    // byte strides: blocks (< 2^32, checked by the host) and token rows
+    const uint32_t kblk = (uint32_t)(p.k_sb * CEB), vblk = (uint32_t)(p.v_sb * CEB);
+    const uint32_t kst = (uint32_t)(p.k_st * CEB), vst = (uint32_t)(p.v_st * CEB);
     const int bs = p.block_size;
     int64_t win_base = p.bs_shift >= 0 ? (t0 >> p.bs_shift) : t0 / bs;
     int win = load_table_window(p, b, win_base, lane);
 
-    // Resolves tile t's block and issues its K/V loads (straight-line:
-    // masked rows read the zero row).
+    // Resolves tile t's block and issues its K/V loads through buffer
+    // resources whose record count ends at the tile's last valid row: rows
+    // past it (all 16 for a masked block) read as zero, with no per-lane
+    // address select and no branch around the loads.
     auto issue = [&](int t, Tile &T) {
       const int64_t base = t0 + (int64_t)t * TILE;
       const int64_t lb = p.bs_shift >= 0 ? (base >> p.bs_shift) : base / bs;
@@ -192,50 +200,53 @@ struct WaveTiles {
         win_base = lb;
         win = load_table_window(p, b, win_base, lane);
       }
-      const int64_t off = base - lb * bs;
+      const uint32_t off = (uint32_t)(base - lb * bs);
       const int phys = __builtin_amdgcn_readlane(win, (int)(lb - win_base));
       const int64_t left = t1 - base;
-      T.n_valid = phys < 0 || left <= 0 ? 0 : (left >= TILE ? TILE : (int)left);
-      const int64_t kro = ((int64_t)phys * p.k_sb + off * p.k_st) * CEB;
-      const int64_t vro = ((int64_t)phys * p.v_sb + off * p.v_st) * CEB;
-      const bool k_ok = hl < T.n_valid;
-      const char *kr = k_ok ? kbase + kro + k_lane : zero_row;
+      const int nv = phys < 0 || left <= 0 ? 0 : (left >= TILE ? TILE : (int)left);
+      T.n_valid = nv;
+      const uint32_t pu = phys < 0 ? 0u : (uint32_t)phys;
+      const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)(kbase + (uint64_t)pu * kblk + off * kst), (short)0, (int)(nv * kst), 0x00020000);
+      const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)(vbase + (uint64_t)pu * vblk + off * vst), (short)0, (int)(nv * vst), 0x00020000);
       if constexpr (KV8) {
         // KSTEPS contiguous 8-byte chunks at 8 KSTEPS grp: paired into
-        // 16-byte loads when KSTEPS is even (then 16-byte aligned), else
-        // 8-byte loads. T.k[s & ~1] holds k-step s (dwords xy for even s).
+        // 16-byte loads when KSTEPS is even, else 8-byte loads. T.k[s & ~1]
+        // holds k-step s (dwords xy for even s).
         if constexpr (KSTEPS % 2 == 0) {
-          const int kstep = k_ok ? 16 : 0;
 #pragma unroll
-          for (int s = 0; s < KSTEPS; s += 2) T.k[s] = load16v_stream(kr + (s / 2) * kstep);
+          for (int s = 0; s < KSTEPS; s += 2) T.k[s] = __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 8 * s, 0, CPOL_NT);
         } else {
-          const int kstep = k_ok ? 8 : 0;
 #pragma unroll
           for (int s = 0; s < KSTEPS; ++s) {
-            const u32x2v w = __builtin_nontemporal_load((global_u32x2_ptr)(kr + s * kstep));
+            const u32x2v w = __builtin_amdgcn_raw_buffer_load_b64(kr, k_lane + 8 * s, 0, CPOL_NT);
             if (s % 2 == 0) T.k[s] = v4u32{w.x, w.y, 0u, 0u};
             else T.k[s - 1] = v4u32{T.k[s - 1].x, T.k[s - 1].y, w.x, w.y};
           }
         }
-        // scales of tokens 4 grp .. +3 (16 bytes; a masked tile reads the zero row)
-        const bool s_ok = T.n_valid > 0;
-        const int64_t so = ((int64_t)phys * p.s_sb + (int64_t)kvh * p.s_sh + off + 4 * grp) * 4;
-        T.ks = __builtin_bit_cast(f32x4_t, load16v_stream(s_ok ? (const char *)p.k_scale + so : zero_row));
-        T.vs = __builtin_bit_cast(f32x4_t, load16v_stream(s_ok ? (const char *)p.v_scale + so : zero_row));
+        // scales of tokens 4 grp .. +3 of the tile's block (16 bytes; a
+        // masked block reads zero)
+        const uint64_t so = (uint64_t)pu * (uint32_t)(p.s_sb * 4) + (uint32_t)(kvh * p.s_sh * 4) + off * 4;
+        const int sn = nv > 0 ? 64 : 0;
+        const __amdgpu_buffer_rsrc_t ksr =
+            __builtin_amdgcn_make_buffer_rsrc((void *)((const char *)p.k_scale + so), (short)0, sn, 0x00020000);
+        const __amdgpu_buffer_rsrc_t vsr =
+            __builtin_amdgcn_make_buffer_rsrc((void *)((const char *)p.v_scale + so), (short)0, sn, 0x00020000);
+        T.ks = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ksr, 16 * grp, 0, CPOL_NT));
+        T.vs = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vsr, 16 * grp, 0, CPOL_NT));
       } else {
-        const int kstep = k_ok ? 64 : 0;
 #pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) T.k[s] = load16v_stream(kr + s * kstep);
+        for (int s = 0; s < KSTEPS; ++s) T.k[s] = __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * s, 0, CPOL_NT);
       }
 #pragma unroll
-      for (int u = 0; u < VLOADS; ++u) {
-        const int row = (u * 64 + lane) / CPIECES;
-        const bool v_ok = row < T.n_valid;
-        T.v[u] = load16v_stream(v_ok ? vbase + vro + v_lane[u] : zero_row);
-      }
+      for (int u = 0; u < VLOADS; ++u) T.v[u] = __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane[u], 0, CPOL_NT);
     };
 
-    auto compute = [&](Tile &T) {
+    // MASK: the tile has fewer than 16 valid rows (the run's last tile, or
+    // a masked block); full tiles skip the masking.
+    auto compute = [&](Tile &T, auto mask) {
+      constexpr bool MASK = decltype(mask)::value;
       // stage V row-major in LDS (rows past the tile are never read)
 #pragma unroll
       for (int u = 0; u < VLOADS; ++u) {
@@ -273,7 +284,7 @@ struct WaveTiles {
       if constexpr (KV8) {
         kscale = T.ks * p.scale_log2;
         vscale = T.vs;
-        if (T.n_valid < TILE) {
+        if constexpr (MASK) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) vscale[i] = 4 * grp + i < T.n_valid ? vscale[i] : 0.f;
         }
@@ -285,7 +296,7 @@ struct WaveTiles {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           sc[i] = sa[g][i] * kscale[i];
-          if (T.n_valid < TILE) sc[i] = 4 * grp + i < T.n_valid ? sc[i] : -INFINITY;
+          if constexpr (MASK) sc[i] = 4 * grp + i < T.n_valid ? sc[i] : -INFINITY;
         }
         float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
         tmax = max_xor32(max_xor16(tmax));
@@ -330,14 +341,18 @@ struct WaveTiles {
       }
     };
 
+    auto run = [&](Tile &T) {
+      if (T.n_valid == TILE) compute(T, std::false_type{});
+      else compute(T, std::true_type{});
+    };
     // software pipeline: the next tile's loads fly while a tile computes
     Tile ta, tb;
     issue(0, ta);
     for (int t = 0; t < n_tiles; t += 2) {
       issue(t + 1, tb);
-      compute(ta);
+      run(ta);
       issue(t + 2, ta);
-      if (t + 1 < n_tiles) compute(tb);
+      if (t + 1 < n_tiles) run(tb);
     }
     // combine the four lane groups' sums (m is already common to them)
 #pragma unroll
