@@ -577,6 +577,166 @@ def run_prefill(args, device) -> int:
     return 0
 
 
+# ------------------------------------------------------------------ sweep
+# The reference's attention sweep (docs/benchmark_report.md:28-34; cases
+# built by benchmark.py:73-123): batch {1, 4, 16} x context {128, 512, 2048}
+# x KV heads {32, 8, 1} (MHA / GQA / MQA) x {fp16, bf16}, 32 query heads,
+# head_dim 64, block 16, warmup 10, 50 event-timed samples.
+SWEEP_BATCHES = (1, 4, 16)
+SWEEP_CONTEXTS = (128, 512, 2048)
+SWEEP_KV_HEADS = (32, 8, 1)
+SWEEP_DTYPES = (("fp16", torch.float16), ("bf16", torch.bfloat16))
+
+# Published A100-SXM4-40GB means (µs) of the reference's triton_paged kernel
+# and of its paged gather + SDPA path on each sweep shape, one line of
+# docs/benchmark_results/a100_cuda13_triton36.jsonl each (lines 1-54).
+A100_SWEEP_US = {
+    ("fp16", 1, 128, 32): (101.3, 184.7), ("bf16", 1, 128, 32): (101.2, 186.2),
+    ("fp16", 1, 128, 8): (102.0, 192.5), ("bf16", 1, 128, 8): (100.6, 191.5),
+    ("fp16", 1, 128, 1): (101.8, 194.9), ("bf16", 1, 128, 1): (101.0, 189.1),
+    ("fp16", 1, 512, 32): (102.5, 196.4), ("bf16", 1, 512, 32): (101.5, 194.9),
+    ("fp16", 1, 512, 8): (102.6, 201.7), ("bf16", 1, 512, 8): (102.4, 204.3),
+    ("fp16", 1, 512, 1): (103.9, 203.3), ("bf16", 1, 512, 1): (102.0, 202.4),
+    ("fp16", 1, 2048, 32): (157.5, 238.4), ("bf16", 1, 2048, 32): (162.1, 238.7),
+    ("fp16", 1, 2048, 8): (146.5, 203.9), ("bf16", 1, 2048, 8): (145.6, 204.3),
+    ("fp16", 1, 2048, 1): (145.5, 204.0), ("bf16", 1, 2048, 1): (146.6, 200.7),
+    ("fp16", 4, 128, 32): (104.2, 224.0), ("bf16", 4, 128, 32): (101.3, 223.8),
+    ("fp16", 4, 128, 8): (101.3, 230.8), ("bf16", 4, 128, 8): (100.3, 230.2),
+    ("fp16", 4, 128, 1): (100.2, 230.2), ("bf16", 4, 128, 1): (99.7, 229.3),
+    ("fp16", 4, 512, 32): (101.7, 270.0), ("bf16", 4, 512, 32): (102.2, 267.9),
+    ("fp16", 4, 512, 8): (101.4, 239.6), ("bf16", 4, 512, 8): (100.8, 237.2),
+    ("fp16", 4, 512, 1): (101.8, 240.4), ("bf16", 4, 512, 1): (101.2, 242.6),
+    ("fp16", 4, 2048, 32): (213.6, 549.9), ("bf16", 4, 2048, 32): (214.1, 606.0),
+    ("fp16", 4, 2048, 8): (164.2, 257.6), ("bf16", 4, 2048, 8): (162.5, 263.4),
+    ("fp16", 4, 2048, 1): (158.0, 240.4), ("bf16", 4, 2048, 1): (156.6, 243.0),
+    ("fp16", 16, 128, 32): (100.7, 271.5), ("bf16", 16, 128, 32): (100.9, 272.2),
+    ("fp16", 16, 128, 8): (100.7, 233.0), ("bf16", 16, 128, 8): (102.2, 233.7),
+    ("fp16", 16, 128, 1): (101.1, 232.7), ("bf16", 16, 128, 1): (105.5, 232.9),
+    ("fp16", 16, 512, 32): (141.0, 617.3), ("bf16", 16, 512, 32): (141.7, 615.1),
+    ("fp16", 16, 512, 8): (117.0, 271.0), ("bf16", 16, 512, 8): (112.3, 270.9),
+    ("fp16", 16, 512, 1): (111.8, 240.0), ("bf16", 16, 512, 1): (112.1, 238.4),
+    ("fp16", 16, 2048, 32): (296.0, 1645.3), ("bf16", 16, 2048, 32): (295.5, 1648.8),
+    ("fp16", 16, 2048, 8): (216.6, 526.5), ("bf16", 16, 2048, 8): (216.6, 525.6),
+    ("fp16", 16, 2048, 1): (190.4, 242.3), ("bf16", 16, 2048, 1): (192.4, 239.8),
+}
+
+
+def build_sweep_case(batch: int, ctx: int, kv_heads: int, dtype: torch.dtype, device: torch.device,
+                     seed: int = 0, heads: int = 32, head_dim: int = 64, block_size: int = 16):
+    """One sweep case with the reference's block-table layout
+    (benchmark.py:85-95): logical block j of request r is physical block
+    j * (B + 1) + r — requests interleaved, one reserved block between
+    rounds — in a pool of exactly the blocks that allocation touches."""
+    from inferkernellab_amd import PagedKVCache
+
+    need = -(-ctx // block_size)
+    pool = batch * need + need - 1
+    tables = [[j * (batch + 1) + r for j in range(need)] for r in range(batch)]
+    cache = PagedKVCache(pool, block_size, kv_heads, head_dim, dtype=dtype, device=device)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    for t in (cache.k, cache.v):
+        t.normal_(0.0, 1.0, generator=gen)
+    query = torch.randn(batch, heads, head_dim, generator=gen, device=device, dtype=torch.float32).to(dtype)
+    return {
+        "cache": cache, "query": query, "tables_list": tables, "lengths": [ctx] * batch,
+        "tables": torch.tensor(tables, dtype=torch.int64, device=device),
+        "lens": torch.tensor([ctx] * batch, dtype=torch.int32, device=device),
+        "dtype": dtype, "fp8": False, "heads": heads, "kv_heads": kv_heads, "head_dim": head_dim,
+        "block_size": block_size, "pool": pool,
+    }
+
+
+def _percentile(values, q: float) -> float:
+    """Linear-interpolated percentile, as the reference reports (benchmark.py:36-44)."""
+    v = sorted(values)
+    pos = (len(v) - 1) * q
+    lo, hi = math.floor(pos), math.ceil(pos)
+    return v[lo] if lo == hi else v[lo] * (hi - pos) + v[hi] * (pos - lo)
+
+
+def run_sweep(args, device) -> int:
+    """Every sweep shape: one checked launch against the oracle (all
+    requests and heads; a mismatch stops the sweep, as the reference's
+    harness raises, benchmark.py:225-268), then warmup and event-timed
+    samples of the whole attention operation (split kernel + reduce) on
+    prevalidated inputs, as the reference times its kernel with
+    validate_inputs=False (benchmark.py:251-262). A 512 MiB MALL flush runs
+    before every sample, outside the event bracket, unless --mall-flush off.
+    One JSON line per shape goes to --sweep-out (and stderr); stdout gets one
+    summary line."""
+    import statistics
+
+    from inferkernellab_amd import ops
+
+    flush_buf = torch.empty(512 << 20, dtype=torch.uint8, device=device) if args.mall_flush != "off" else None
+    rows = []
+    out_file = open(args.sweep_out, "w") if args.sweep_out else None
+    for name, dtype in SWEEP_DTYPES:
+        for batch in SWEEP_BATCHES:
+            for ctx in SWEEP_CONTEXTS:
+                for kv in SWEEP_KV_HEADS:
+                    w = build_sweep_case(batch, ctx, kv, dtype, device, args.seed)
+                    attn = ops.PreparedPagedAttention(w["query"], w["cache"], w["tables"], w["lens"],
+                                                      max_context_len=ctx)
+                    attn()
+                    torch.cuda.synchronize()
+                    check = parity(attn.out, oracle_step(oracle_view(w), w), dtype)
+                    shape = {"dtype": name, "batch": batch, "context_len": ctx, "num_heads": 32,
+                             "num_kv_heads": kv, "head_dim": 64, "block_size": 16, "num_blocks": w["pool"]}
+                    if not check["passed"]:
+                        print(json.dumps({"error": "sweep case differs from the oracle", "case": shape,
+                                          "parity": check}))
+                        return 3
+                    for _ in range(args.warmup):
+                        attn()
+                    samples = []
+                    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    for i in range(args.steps):
+                        if flush_buf is not None:
+                            flush_buf.fill_(i & 0xFF)
+                        start.record()
+                        attn()
+                        stop.record()
+                        stop.synchronize()
+                        samples.append(start.elapsed_time(stop) * 1e3)
+                    mean_us = sum(samples) / len(samples)
+                    a100_triton, a100_sdpa = A100_SWEEP_US[(name, batch, ctx, kv)]
+                    kv_bytes = 2 * batch * ctx * kv * 64 * 2  # the reference's estimated_kv_read_bytes
+                    row = {
+                        "case": shape, "path": attn.path,
+                        "split": "balanced" if attn.balanced_split else (
+                            f"fixed {attn.partition_size}" if attn.partition_size > 0 else "none"),
+                        "mean_us": round(mean_us, 2), "p50_us": round(_percentile(samples, 0.5), 2),
+                        "p95_us": round(_percentile(samples, 0.95), 2),
+                        "kv_gbps": round(kv_bytes / (mean_us * 1e-6) / 1e9, 1),
+                        "max_abs_err": check["max_abs_err"], "tolerance": check["tolerance"],
+                        "a100_triton_us": a100_triton, "a100_paged_sdpa_us": a100_sdpa,
+                        "speedup_vs_a100_triton": round(a100_triton / mean_us, 2),
+                    }
+                    rows.append(row)
+                    line = json.dumps(row)
+                    print(line, file=sys.stderr, flush=True)
+                    if out_file:
+                        out_file.write(line + "\n")
+                    del attn, w
+    if out_file:
+        out_file.close()
+    ratios = [r["speedup_vs_a100_triton"] for r in rows]
+    print(json.dumps({
+        "sweep": "reference attention matrix: batch {1,4,16} x context {128,512,2048} x kv heads "
+                 "{32,8,1} x {fp16,bf16}; 32 heads, head_dim 64, block 16",
+        "cases": len(rows),
+        "all_within_tolerance": True,
+        "max_abs_err": {n: max(r["max_abs_err"] for r in rows if r["case"]["dtype"] == n) for n, _ in SWEEP_DTYPES},
+        "median_speedup_vs_a100_triton": round(statistics.median(ratios), 2),
+        "min_speedup_vs_a100_triton": min(ratios),
+        "max_speedup_vs_a100_triton": max(ratios),
+        "mall_flush": flush_buf is not None,
+        "samples": args.steps, "warmup": args.warmup,
+    }))
+    return 0
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -603,6 +763,10 @@ def main() -> int:
     parser.add_argument("--copy-calibration", action="store_true",
                         help="run only a plain 512 MiB device copy (torch copy_) three times: the "
                              "known-size reference for scaling FETCH_SIZE / WRITE_SIZE counters")
+    parser.add_argument("--sweep", action="store_true",
+                        help="run the reference's 54-shape attention sweep (each shape checked against "
+                             "the oracle, then timed; --steps samples after --warmup launches)")
+    parser.add_argument("--sweep-out", default=None, help="JSONL file for the sweep's per-shape records")
     args = parser.parse_args()
 
     if args.gpus != 1:
@@ -625,6 +789,8 @@ def main() -> int:
         print(json.dumps({"copy_calibration": {"bytes_read": nbytes, "bytes_written": nbytes, "launches": 3}}))
         return 0
 
+    if args.sweep:
+        return run_sweep(args, device)
     if args.workload in PREFILL_WORKLOADS:
         return run_prefill(args, device)
 

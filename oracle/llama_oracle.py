@@ -21,6 +21,13 @@ architecture of the Transformers model the reference loads):
 * MLP: ``down(silu(gate(x)) * up(x))``; residual adds around both blocks;
   final norm, then ``lm_head``.
 
+``round_to="bfloat16"`` (or ``"float16"``) restates a model run in that
+dtype: every op's output is rounded to it where torch's ops on such tensors
+round (linear layers, RMSNorm's normalised rows and its weight product, the
+RoPE tables and each term and sum of the rotation, the attention output,
+residual adds, SiLU and the gate product, the logits); the attention itself
+stays float32, as the paged kernels compute it.
+
 Parity pins (tests/test_llama_oracle.py): Transformers' ``LlamaForCausalLM``
 (eager attention, float32, CPU) on the same weights; a zero-layer model is
 ``lm_head(norm(embedding))``; RoPE is norm-preserving, the identity at
@@ -32,29 +39,47 @@ from __future__ import annotations
 
 import numpy as np
 
+from oracle.paged_oracle import bf16_bits_to_f32, f32_to_bf16_bits
+
 
 def weights_from_model(model) -> dict:
     """float32 numpy copies of a Llama model's parameters (exact for bf16/fp16)."""
     return {name: p.detach().float().cpu().numpy() for name, p in model.named_parameters()}
 
 
-def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+def rounder(dtype: str | None):
+    """x -> x rounded to `dtype` and widened back to float32 (identity for None / float32)."""
+    if dtype in (None, "float32"):
+        return lambda x: np.asarray(x, dtype=np.float32)
+    if dtype == "bfloat16":
+        return lambda x: bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(x, dtype=np.float32)))
+    if dtype == "float16":
+        return lambda x: np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+    raise ValueError(f"unsupported dtype: {dtype}")
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float, r=rounder(None)) -> np.ndarray:
+    """Normalised in float32, rounded, then the weight product rounded."""
     x = x.astype(np.float32)
-    return (x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + np.float32(eps))) * w
+    return r(w * r(x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + np.float32(eps))))
 
 
-def rope_tables(positions: np.ndarray, head_dim: int, theta: float):
-    inv = 1.0 / (theta ** (np.arange(0, head_dim, 2, dtype=np.float32) / head_dim))
+def rope_tables(positions: np.ndarray, head_dim: int, theta: float, r=rounder(None)):
+    """float32 cos / sin [T, D]. The inverse frequencies pass through `r`:
+    a model converted to a 16-bit dtype holds them in that dtype (they are a
+    floating-point buffer of the module), and its angles are float32
+    products of those rounded values."""
+    inv = r(1.0 / (theta ** (np.arange(0, head_dim, 2, dtype=np.float32) / head_dim)))
     ang = positions.astype(np.float32)[:, None] * inv.astype(np.float32)[None, :]
     ang = np.concatenate([ang, ang], axis=-1)
     return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
 
 
-def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
-    """x [T, heads, D]; cos/sin [T, D]."""
+def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, r=rounder(None)) -> np.ndarray:
+    """x [T, heads, D]; cos/sin [T, D] (already in the run's dtype)."""
     half = x.shape[-1] // 2
     rot = np.concatenate([-x[..., half:], x[..., :half]], axis=-1)
-    return x * cos[:, None, :] + rot * sin[:, None, :]
+    return r(r(x * cos[:, None, :]) + r(rot * sin[:, None, :]))
 
 
 def causal_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray) -> np.ndarray:
@@ -71,31 +96,35 @@ def causal_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray) -> np.ndarray:
     return np.matmul(p, vv).transpose(1, 0, 2).astype(np.float32)
 
 
-def full_sequence_logits(w: dict, config, token_ids) -> np.ndarray:
-    """float32 logits [T, vocab] of a causal forward over `token_ids`."""
+def full_sequence_logits(w: dict, config, token_ids, round_to: str | None = None) -> np.ndarray:
+    """float32 logits [T, vocab] of a causal forward over `token_ids`
+    (with `round_to`, of a run in that dtype)."""
+    r = rounder(round_to)
     ids = np.asarray(token_ids, dtype=np.int64)
     h_heads, kv_heads = int(config.num_attention_heads), int(config.num_key_value_heads)
     d = int(getattr(config, "head_dim", None) or config.hidden_size // h_heads)
     eps = float(config.rms_norm_eps)
-    cos, sin = rope_tables(np.arange(len(ids)), d, float(config.rope_theta))
-    x = w["model.embed_tokens.weight"][ids].astype(np.float32)
+    cos, sin = rope_tables(np.arange(len(ids)), d, float(config.rope_theta), r)
+    cos, sin = r(cos), r(sin)
+    x = r(w["model.embed_tokens.weight"][ids])
     for i in range(int(config.num_hidden_layers)):
         p = f"model.layers.{i}."
-        a = rmsnorm(x, w[p + "input_layernorm.weight"], eps)
-        q = (a @ w[p + "self_attn.q_proj.weight"].T).reshape(len(ids), h_heads, d)
-        k = (a @ w[p + "self_attn.k_proj.weight"].T).reshape(len(ids), kv_heads, d)
-        v = (a @ w[p + "self_attn.v_proj.weight"].T).reshape(len(ids), kv_heads, d)
-        o = causal_attention(rope(q, cos, sin), rope(k, cos, sin), v)
-        x = x + o.reshape(len(ids), h_heads * d) @ w[p + "self_attn.o_proj.weight"].T
-        m = rmsnorm(x, w[p + "post_attention_layernorm.weight"], eps)
-        g = m @ w[p + "mlp.gate_proj.weight"].T
-        x = x + ((g / (1.0 + np.exp(-g))) * (m @ w[p + "mlp.up_proj.weight"].T)) @ w[p + "mlp.down_proj.weight"].T
-    x = rmsnorm(x, w["model.norm.weight"], eps)
-    return (x @ w["lm_head.weight"].T).astype(np.float32)
+        a = rmsnorm(x, w[p + "input_layernorm.weight"], eps, r)
+        q = r(a @ w[p + "self_attn.q_proj.weight"].T).reshape(len(ids), h_heads, d)
+        k = r(a @ w[p + "self_attn.k_proj.weight"].T).reshape(len(ids), kv_heads, d)
+        v = r(a @ w[p + "self_attn.v_proj.weight"].T).reshape(len(ids), kv_heads, d)
+        o = r(causal_attention(rope(q, cos, sin, r), rope(k, cos, sin, r), v))
+        x = r(x + r(o.reshape(len(ids), h_heads * d) @ w[p + "self_attn.o_proj.weight"].T))
+        m = rmsnorm(x, w[p + "post_attention_layernorm.weight"], eps, r)
+        g = r(m @ w[p + "mlp.gate_proj.weight"].T)
+        act = r(r(g / (1.0 + np.exp(-g))) * r(m @ w[p + "mlp.up_proj.weight"].T))
+        x = r(x + r(act @ w[p + "mlp.down_proj.weight"].T))
+    x = rmsnorm(x, w["model.norm.weight"], eps, r)
+    return r(x @ w["lm_head.weight"].T).astype(np.float32)
 
 
-def teacher_forced_logits(w: dict, config, prompt, generated) -> np.ndarray:
+def teacher_forced_logits(w: dict, config, prompt, generated, round_to: str | None = None) -> np.ndarray:
     """[len(generated), vocab]: row j = logits that choose generated[j]."""
     seq = list(prompt) + list(generated[:-1])
-    logits = full_sequence_logits(w, config, seq)
+    logits = full_sequence_logits(w, config, seq, round_to)
     return logits[len(prompt) - 1:]

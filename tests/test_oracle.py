@@ -239,6 +239,40 @@ def test_bench_bytes_formula_matches_reference_kv_term():
     assert math.isclose(total / kv, 1.0, rel_tol=0.01)
 
 
+@pytest.mark.parametrize("batch,ctx", [(1, 128), (4, 512), (16, 2048), (3, 100)])
+def test_bench_sweep_tables_follow_the_reference_allocation_order(batch, ctx):
+    """The sweep's closed-form tables equal what the block allocator hands
+    out in the reference's case construction (benchmark.py:85-95): one block
+    per request per logical block, then one reserved block between rounds;
+    the pool is exactly the blocks that allocation touches (e.g. 15 for
+    batch 1 x 128 and 2175 for batch 16 x 2048, as the reference's A100
+    records state)."""
+    import bench
+    from inferkernellab_amd.cache import BlockAllocator
+
+    w = bench.build_sweep_case(batch, ctx, 8, torch.float16, torch.device("cpu"))
+    need = -(-ctx // 16)
+    alloc = BlockAllocator(w["pool"])
+    tables = [[] for _ in range(batch)]
+    for j in range(need):
+        for r in range(batch):
+            tables[r].extend(alloc.allocate(1, owner=r))
+        if j + 1 < need:
+            alloc.allocate(1, owner=-1)
+    assert w["tables_list"] == tables
+    assert alloc.num_free_blocks == 0
+    assert {(1, 128): 15, (16, 2048): 2175}.get((batch, ctx), w["pool"]) == w["pool"]
+
+
+def test_bench_sweep_covers_the_published_matrix():
+    """Every one of the 54 sweep shapes has its published A100 timings."""
+    import bench
+
+    shapes = {(n, b, c, kv) for n, _ in bench.SWEEP_DTYPES for b in bench.SWEEP_BATCHES
+              for c in bench.SWEEP_CONTEXTS for kv in bench.SWEEP_KV_HEADS}
+    assert len(shapes) == 54 and shapes == set(bench.A100_SWEEP_US)
+
+
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16", "float32"])
 def test_rope_rows_match_torch_ops_bit_for_bit(dtype):
     """rope_rows against torch's elementwise sequence of hf_benchmark.py:69-85
