@@ -22,7 +22,8 @@ sample of the same requests.
 
 Workloads whose step K/V is below 512 MiB (everything but the default) fit
 in the 256 MB MALL, so by default (``--mall-flush auto``) a 512 MiB buffer
-is written before every timed sample: outside the HIP-event brackets of the
+is read before every timed sample (a read, so that no dirty lines are left
+to write back during the sample): outside the HIP-event brackets of the
 kernels, and its own event-timed duration is taken out of the step's wall
 time.
 
@@ -95,6 +96,23 @@ class HipEvents:
 
     def destroy(self, handle: int) -> None:
         self.lib.hipEventDestroy(ctypes.c_void_p(handle))
+
+
+class MallFlush:
+    """Evicts the 256 MB MALL (and the L2s) before a timed sample by READING
+    a 512 MiB buffer (one reduction over it), so that the flush leaves no
+    dirty lines whose write-back could compete with the sample's own reads
+    (on a read-only probe of the MQA workload's 90 MB of K/V tiles, a 512 MiB
+    hipMemsetAsync before each launch doubled its time, 19 -> 37 µs, against
+    the read flush); a decode step's attention follows reads of other
+    layers' K/V and weights, not bulk writes."""
+
+    def __init__(self, device: torch.device):
+        self.buf = torch.zeros((512 << 20) // 4, dtype=torch.float32, device=device)
+        self.sink = torch.empty((), dtype=torch.float32, device=device)
+
+    def __call__(self) -> None:
+        torch.sum(self.buf, dim=0, out=self.sink)
 
 
 def build_workload(name: str, device: torch.device, seed: int = 0, head_major: bool | None = None):
@@ -660,15 +678,15 @@ def run_sweep(args, device) -> int:
     harness raises, benchmark.py:225-268), then warmup and event-timed
     samples of the whole attention operation (split kernel + reduce) on
     prevalidated inputs, as the reference times its kernel with
-    validate_inputs=False (benchmark.py:251-262). A 512 MiB MALL flush runs
-    before every sample, outside the event bracket, unless --mall-flush off.
+    validate_inputs=False (benchmark.py:251-262). A 512 MiB MALL flush (a
+    read) runs before every sample, outside the event bracket, unless --mall-flush off.
     One JSON line per shape goes to --sweep-out (and stderr); stdout gets one
     summary line."""
     import statistics
 
     from inferkernellab_amd import ops
 
-    flush_buf = torch.empty(512 << 20, dtype=torch.uint8, device=device) if args.mall_flush != "off" else None
+    flush_buf = MallFlush(device) if args.mall_flush != "off" else None
     rows = []
     out_file = open(args.sweep_out, "w") if args.sweep_out else None
     for name, dtype in SWEEP_DTYPES:
@@ -693,7 +711,7 @@ def run_sweep(args, device) -> int:
                     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                     for i in range(args.steps):
                         if flush_buf is not None:
-                            flush_buf.fill_(i & 0xFF)
+                            flush_buf()
                         start.record()
                         attn()
                         stop.record()
@@ -757,7 +775,7 @@ def main() -> int:
     parser.add_argument("--no-graph", action="store_true",
                         help="time eager launches instead of HIP graph replays of the step")
     parser.add_argument("--mall-flush", choices=("auto", "on", "off"), default="auto",
-                        help="write a 512 MiB buffer before every timed sample so that the K/V of "
+                        help="read a 512 MiB buffer before every timed sample so that the K/V of "
                              "the step is not served from the 256 MB MALL (auto: when the step's "
                              "K/V is below 512 MiB, i.e. every workload but the 805 MB GQA one)")
     parser.add_argument("--copy-calibration", action="store_true",
@@ -821,17 +839,17 @@ def main() -> int:
     ev = [[events.create() for _ in range(3)] for _ in range(k_steps)]
     attn_bytes, append_bytes = step_bytes(w)
     flush = args.mall_flush == "on" or (args.mall_flush == "auto" and attn_bytes < (512 << 20))
-    flush_buf = torch.empty(512 << 20, dtype=torch.uint8, device=device) if flush else None
+    flush_buf = MallFlush(device) if flush else None
 
     flush_marks = []
 
     def flush_mall(i: int) -> None:
-        """512 MiB of writes (evicts the MALL and the L2s), bracketed by
+        """512 MiB of reads (evicts the MALL and the L2s), bracketed by
         events so that the step time can leave it out."""
         if flush_buf is not None:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-            flush_buf.fill_(i & 0xFF)
+            flush_buf()
             e1.record()
             flush_marks.append((e0, e1))
 
@@ -962,7 +980,7 @@ def main() -> int:
         "us_per_step": round(ms_per_step * 1e3, 1),
         "step_mode": step_mode,
         "step_timing": ("wall clock around the K steps, synchronized on both sides, minus the "
-                        "event-timed 512 MiB MALL flush written before each step" if flush
+                        "event-timed 512 MiB MALL flush read before each step" if flush
                         else "wall clock around the K steps, synchronized on both sides"),
         "eager_us_per_step": round(eager_wall_s * 1e6 / k_steps, 1),
         "one_step_graph_us_per_step": round(single_graph_us, 1) if single_graph_us is not None else None,

@@ -39,15 +39,14 @@ namespace {
 constexpr int TILE = 16;  // tokens per tile
 constexpr int CPOL_NT = 2;  // buffer-load cache policy: non-temporal (K/V rows are read once)
 
-// Register budget: the FP8 kernels with 16-head units ask for at least 2
-// waves per SIMD (VGPRs + AGPRs <= 256): they then keep their accumulators
-// in VGPRs, without the accumulator-register copies the compiler otherwise
-// places in every tile (81 -> 78 us on the FP8 GQA decode workload). The
-// others keep the compiler's choice (the 32-head kernels would spill; the
-// 16-bit 16-head ones fit two waves anyway). Two waves per SIMD for the
-// fixed-partition 32-head kernel (217 VGPRs without the split masking
-// path) measured slower on MQA: 31.0 against 28.4 us.
-#define IKL_MFMA_WAVES_ATTR __attribute__((amdgpu_waves_per_eu(KV8 && NG == 1 ? 2 : 1, 8)))
+// Register budget: kernels with 16-head units ask for at least 2 waves per
+// SIMD (VGPRs + AGPRs <= 256); the allocator then keeps their accumulators
+// in VGPRs, without the accumulator-register copies it otherwise places in
+// every tile (81 -> 78 us on the FP8 GQA decode workload). The 32-head
+// kernels of the fixed partitions keep the compiler's choice (one wave per
+// SIMD: at two they would spill; two waves per SIMD at 217 VGPRs without
+// the split masking path measured slower on MQA, 31.0 against 28.4 us).
+#define IKL_MFMA_WAVES_ATTR __attribute__((amdgpu_waves_per_eu(NG == 1 ? 2 : 1, 8)))
 
 // bf16 P enters the PV product with its rounding residual in a second MFMA
 // (fp16 P, <= 2^8, already keeps 11 bits and is not split). The FP8 cache
@@ -492,6 +491,90 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
   }
 }
 
+// Start of balanced-split run w: the batch's total tiles T (units x
+// request tiles), the run [g0, g1) = [w T / W, (w + 1) T / W) with W =
+// min(sk_waves, T), and the request b holding tile g0 with its tile count nb
+// and the tiles pb of the requests before it. Every lane of the calling
+// wave gets the same values; `active` is false for runs past W.
+struct SkRun {
+  int64_t g0, g1, b, pb;
+  int nb;
+  bool active;
+};
+
+// The value of lane 0 (every lane of the wave holds the same one), in
+// scalar registers: the split's bookkeeping comes out of cross-lane ops
+// the compiler cannot prove uniform, and without this every buffer
+// resource built from it (one per tile) would be wrapped in a loop over
+// distinct lane values around each K/V load.
+__device__ __forceinline__ int64_t uniform64(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ SkRun sk_run(const AttnParams &p, int64_t w, int lane) {
+  SkRun r{0, 0, -1, 0, 0, false};
+  const int64_t U = p.units;
+  // total tiles, then the request holding the run's first tile (a batch
+  // of up to 64 requests takes one scan for both)
+  int64_t total;
+  int n1 = 0, incl1 = 0;
+  if (p.batch <= 64) {
+    n1 = lane < p.batch ? (int)((clamped_ctx(p, lane) + 15) >> 4) : 0;
+    incl1 = wave_incl_scan(n1, lane);
+    total = __builtin_amdgcn_readlane(incl1, 63);
+  } else {
+    int64_t before0;
+    int own0;
+    total = request_tiles(p, 0, lane, &before0, &own0);
+  }
+  const int64_t T = U * total;
+  const int64_t W = (int64_t)p.sk_waves < T ? (int64_t)p.sk_waves : T;
+  if (w >= W) return r;
+  r.active = true;
+  r.g0 = w * T / W;
+  r.g1 = (w + 1) * T / W;
+
+  if (p.batch <= 64) {
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < p.batch && U * incl1 > r.g0);
+    const int l = __builtin_ctzll(hit);  // g0 < T: some request's tiles end past it
+    r.b = l;
+    r.nb = __shfl(n1, l, 64);
+    r.pb = __shfl(incl1, l, 64) - r.nb;
+  }
+  int64_t base = 0;
+  for (int64_t c0 = 0; c0 < p.batch && r.b < 0; c0 += 64) {
+    const int64_t q = c0 + lane;
+    const int n = q < p.batch ? (int)((clamped_ctx(p, q) + 15) >> 4) : 0;
+    const int incl = wave_incl_scan(n, lane);
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(q < p.batch && U * (base + incl) > r.g0);
+    if (hit) {
+      const int l = __builtin_ctzll(hit);
+      r.b = c0 + l;
+      r.nb = __shfl(n, l, 64);
+      r.pb = base + __shfl(incl, l, 64) - r.nb;
+    }
+    base += __shfl(incl, 63, 64);
+  }
+  r.g0 = uniform64(r.g0);
+  r.g1 = uniform64(r.g1);
+  r.b = uniform64(r.b);
+  r.pb = uniform64(r.pb);
+  r.nb = __builtin_amdgcn_readfirstlane(r.nb);
+  return r;
+}
+
+// Moves a run to the next request with tiles after finishing request b's
+// last unit (one exists while the run has tiles left).
+__device__ __forceinline__ void sk_next_request(const AttnParams &p, int64_t &b, int &nb, int64_t &pb) {
+  do {
+    pb += nb;
+    ++b;
+    nb = __builtin_amdgcn_readfirstlane((int)((clamped_ctx(p, b) + 15) >> 4));
+  } while (nb == 0);
+}
+
 // Balanced split: one wave per workgroup, p.sk_waves workgroups (grid.x).
 // Wave w attends global tiles [w T / W, (w + 1) T / W) of the batch (T =
 // units x tiles of all requests, W = min(sk_waves, T)) piece by piece — a
@@ -505,47 +588,12 @@ __global__ __launch_bounds__(64) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_stre
   __shared__ __attribute__((aligned(16))) char lds[SLOT];
   const int lane = threadIdx.x;
   const int64_t U = p.units;
-
-  // total tiles, then the request holding this wave's first tile (a batch
-  // of up to 64 requests takes one scan for both)
-  int64_t total, b = -1, pb = 0;
-  int nb = 0, n1 = 0, incl1 = 0;
-  if (p.batch <= 64) {
-    n1 = lane < p.batch ? (int)((clamped_ctx(p, lane) + 15) >> 4) : 0;
-    incl1 = wave_incl_scan(n1, lane);
-    total = __builtin_amdgcn_readlane(incl1, 63);
-  } else {
-    int64_t before0;
-    int own0;
-    total = request_tiles(p, 0, lane, &before0, &own0);
-  }
-  const int64_t T = U * total;
-  const int64_t W = (int64_t)p.sk_waves < T ? (int64_t)p.sk_waves : T;
   const int64_t w = blockIdx.x;
-  if (w >= W) return;
-  const int64_t g0 = w * T / W, g1 = (w + 1) * T / W;
-
-  if (p.batch <= 64) {
-    const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < p.batch && U * incl1 > g0);
-    const int l = __builtin_ctzll(hit);  // g0 < T: some request's tiles end past it
-    b = l;
-    nb = __shfl(n1, l, 64);
-    pb = __shfl(incl1, l, 64) - nb;
-  }
-  int64_t base = 0;
-  for (int64_t c0 = 0; c0 < p.batch && b < 0; c0 += 64) {
-    const int64_t r = c0 + lane;
-    const int n = r < p.batch ? (int)((clamped_ctx(p, r) + 15) >> 4) : 0;
-    const int incl = wave_incl_scan(n, lane);
-    const uint64_t hit = __builtin_amdgcn_ballot_w64(r < p.batch && U * (base + incl) > g0);
-    if (hit) {
-      const int l = __builtin_ctzll(hit);
-      b = c0 + l;
-      nb = __shfl(n, l, 64);
-      pb = base + __shfl(incl, l, 64) - nb;
-    }
-    base += __shfl(incl, 63, 64);
-  }
+  const SkRun run = sk_run(p, w, lane);
+  if (!run.active) return;
+  const int64_t g0 = run.g0, g1 = run.g1;
+  int64_t b = run.b, pb = run.pb;
+  int nb = run.nb;
 
   WT wt(p);
   float *const stage = reinterpret_cast<float *>(lds);
@@ -584,13 +632,7 @@ __global__ __launch_bounds__(64) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_stre
 
     g += t_hi - t_in;
     if (g >= g1) break;
-    if (t_hi == nb && u == U - 1) {  // next request with tiles (one exists: g < T)
-      do {
-        pb += nb;
-        ++b;
-        nb = (int)((clamped_ctx(p, b) + 15) >> 4);
-      } while (nb == 0);
-    }
+    if (t_hi == nb && u == U - 1) sk_next_request(p, b, nb, pb);  // one exists: g < T
   }
 }
 
