@@ -319,12 +319,14 @@ def test_llama_e2e_bf16_greedy_tokens_against_cpu_oracle():
     BOUND on every logit of every step. A greedy token can then differ from
     the oracle's argmax only where the oracle's top logit leads the
     generated token's logit by at most 2 * BOUND; every flip is printed with
-    that margin and must satisfy it. The float32 oracle's agreement is
-    reported beside it: a bf16 run cannot follow it (its own rounding moves
-    the prompt logits already by several tenths)."""
+    that margin and must satisfy it, and at least 95 % of all greedy tokens
+    agree (measured: logits within 0.086, 986 / 1024 tokens, every flip a
+    near-tie within 0.047). The float32 oracle's agreement is reported
+    beside it: a bf16 run cannot follow it (180 / 256 measured; its own
+    rounding moves the prompt logits already by several tenths)."""
     from oracle import llama_oracle as lo
 
-    bound = 0.15
+    bound = 0.12
     print("llama e2e bf16 8x2048 b16 p512 n64 vs cpu oracle (bf16 rounding)", flush=True)
     cfg, model, prompts = _e2e_setup(torch.bfloat16)
     result = _e2e_run(model, prompts)
@@ -349,6 +351,7 @@ def test_llama_e2e_bf16_greedy_tokens_against_cpu_oracle():
           f"oracle (requests 0, 4, 8, 12): {agree32}/{4 * 64}", flush=True)
     assert worst <= bound
     assert all(margin <= 2 * bound for *_, margin in flips)
+    assert total - len(flips) >= 0.95 * total
 
 
 def eager_logits(model, tokens) -> torch.Tensor:
