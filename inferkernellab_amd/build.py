@@ -46,8 +46,16 @@ COMMON_FLAGS = [
 
 # Per-source additions. The prefill kernels produce no NaN of their own
 # (masked scores are -inf, never 0/0): without NaN handling, fmaxf skips the
-# IEEE canonicalisation of its operands in the softmax.
-SOURCE_FLAGS = {"paged_prefill.hip": ["-fno-honor-nans"]}
+# IEEE canonicalisation of its operands in the softmax. The decode MFMA
+# kernels keep their matrix accumulators in VGPRs: the 32-head kernels (one
+# wave per SIMD) then lose the accumulator-register copies the allocator
+# otherwise places in every tile (MQA balanced split 29.7 -> 28.6 us); the
+# 16-head kernels already allocate VGPRs only (two waves per SIMD) and are
+# unchanged.
+SOURCE_FLAGS = {
+    "paged_prefill.hip": ["-fno-honor-nans"],
+    "paged_decode_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
 
 
 def _hipcc() -> str:

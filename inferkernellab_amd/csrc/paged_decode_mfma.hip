@@ -43,9 +43,10 @@ constexpr int CPOL_NT = 2;  // buffer-load cache policy: non-temporal (K/V rows 
 // SIMD (VGPRs + AGPRs <= 256); the allocator then keeps their accumulators
 // in VGPRs, without the accumulator-register copies it otherwise places in
 // every tile (81 -> 78 us on the FP8 GQA decode workload). The 32-head
-// kernels of the fixed partitions keep the compiler's choice (one wave per
-// SIMD: at two they would spill; two waves per SIMD at 217 VGPRs without
-// the split masking path measured slower on MQA, 31.0 against 28.4 us).
+// kernels run one wave per SIMD (at two they would spill; two waves per SIMD
+// at 217 VGPRs without the split masking path measured slower on MQA, 31.0
+// against 28.4 us); the build keeps their accumulators in VGPRs as well
+// (-amdgpu-mfma-vgpr-form for this file).
 #define IKL_MFMA_WAVES_ATTR __attribute__((amdgpu_waves_per_eu(NG == 1 ? 2 : 1, 8)))
 
 // bf16 P enters the PV product with its rounding residual in a second MFMA
