@@ -149,3 +149,28 @@ def test_prefill_sweep(i):
     expected = po.paged_prefill_attention(case.query_f32, case.base.oracle_cache, case.base.tables,
                                           cfg["starts"], cfg["ends"])
     assert_close_up_to_output_rounding(got, expected, cfg["dtype"])
+
+
+@pytest.mark.parametrize("dtype_name", ["fp16", "bf16"])
+def test_reference_attention_matrix_matches_oracle(dtype_name):
+    """The reference's 54-shape attention matrix (docs/benchmark_report.md:
+    28-34: batch {1, 4, 16} x context {128, 512, 2048} x KV heads {32, 8, 1},
+    32 heads, head_dim 64, block 16), built by the benchmark's own case
+    builder with the reference's interleaved tables (benchmark.py:85-95):
+    every request and head of the automatic launch against the oracle, at
+    max-abs 2e-3 (fp16) / 1e-2 (bf16) plus half an output ulp (the bench's
+    parity gate, which `bench.py --sweep` applies before timing each shape)."""
+    import bench
+    from inferkernellab_amd import ops
+
+    dtype = dict(bench.SWEEP_DTYPES)[dtype_name]
+    dev = torch.device("cuda", 0)
+    for batch in bench.SWEEP_BATCHES:
+        for ctx in bench.SWEEP_CONTEXTS:
+            for kv in bench.SWEEP_KV_HEADS:
+                print(f"reference matrix {dtype_name} B{batch} ctx{ctx} kv{kv}", flush=True)
+                w = bench.build_sweep_case(batch, ctx, kv, dtype, dev)
+                out = ops.paged_decode_attention_hip(w["query"], w["cache"], w["tables"], w["lens"])
+                torch.cuda.synchronize()
+                check = bench.parity(out, bench.oracle_step(bench.oracle_view(w), w), dtype)
+                assert check["passed"], (batch, ctx, kv, check)
