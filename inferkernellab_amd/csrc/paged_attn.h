@@ -77,6 +77,7 @@ struct AttnParams {
   // slots are distinct and each unit's pieces are consecutive).
   int32_t sk_waves;
   int32_t units;           // kv heads x query groups per request
+  int32_t grid_spread;     // fixed-partition MFMA grid is request-fastest (spread_grid)
   int64_t batch;
   int64_t cap_tokens;      // table_width * block_size: positions a table can map
   // FP8 KV cache (MFMA family): E4M3 codes with one fp32 scale per (token,
@@ -87,6 +88,19 @@ struct AttnParams {
   int64_t s_sb, s_sh;      // elements
   FusedAppend app;         // rows == 0 unless a decode step fuses its append
 };
+
+// Order of the fixed-partition MFMA kernel's grid. Consecutive workgroups
+// are dealt round-robin over the 8 XCDs. The default is unit-fastest (unit,
+// partition, request). When the units are not a multiple of 8 but units x
+// partitions is, that order puts partition i of every request on the same
+// XCD (one unit and 8 partitions: XCD = partition), so ragged context
+// lengths leave the XCDs of the last partitions idle; the grid is then
+// request-fastest (request, unit, partition) with the request rotated by
+// the partition index. Grids of at most 256 workgroups keep the default
+// (request-fastest measured the same or slower there).
+inline bool spread_grid(int64_t units, int64_t parts, int64_t batch) {
+  return (units & 7) != 0 && ((units * parts) & 7) == 0 && units * parts * batch > 256 && units <= 65535;
+}
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

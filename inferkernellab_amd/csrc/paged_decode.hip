@@ -842,6 +842,7 @@ int run_attention(const ikl_paged_attention_args *a, const Plan &pl, const Fused
   p.scale_log2 = a->scale * LOG2E;
   p.sk_waves = pl.sk_waves;
   p.units = (int32_t)pl.units;
+  p.grid_spread = pl.path == IKL_PATH_MFMA_GROUPED && pl.sk_waves == 0 && spread_grid(pl.units, pl.num_parts, a->batch);
   p.batch = a->batch;
   p.cap_tokens = a->table_width * (int64_t)a->block_size;
   p.kv_fp8 = pl.kv_fp8 ? 1 : 0;
