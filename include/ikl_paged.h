@@ -132,8 +132,9 @@ typedef struct ikl_paged_attention_args {
   int32_t query_group_size;
   /* Tokens per split-context partition: 0 = pick automatically, -1 = never
    * split (one pass per request), -2 = the balanced split (MFMA family:
-   * equal runs of the batch's tiles per wave), else a positive multiple of
-   * 64. */
+   * equal runs of the batch's tiles per wave; with path -1 an MHA launch
+   * moves to the MFMA family for it where that supports the shape), else a
+   * positive multiple of 64. */
   int32_t partition_size;
   /* Host-known upper bound of context_lens (0 = table_width*block_size);
    * only sizes the grid, never read from device memory. Contract: every

@@ -536,6 +536,16 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
     pl.path = IKL_PATH_MFMA_GROUPED;
   } else if (a->path == -1) {
     pl.path = select_path(a->dtype, a->head_dim, a->block_size, pl.heads_per_kv, requested_gs);
+    // partition_size -2 asks for the balanced split, which the MFMA family
+    // runs: an MHA launch left to the library moves there from the per-head
+    // kernel when the family supports its shape. On ragged batches the
+    // balanced split beats the per-head kernel's fixed partitions (whole
+    // operation, MALL flushed: MHA 32 hd128 bf16 B32 x U[1024, 4096] 307 ->
+    // 228 us, hd64 fp16 B64 x U[1024, 4096] 303 -> 225 us); on uniform ones
+    // the per-head kernel, which partition_size 0 keeps, is 6-10 % faster.
+    if (a->partition_size == -2 && pl.path == IKL_PATH_MHA_FALLBACK &&
+        mfma_supported(a->dtype, a->head_dim, a->block_size, 1))
+      pl.path = IKL_PATH_MFMA_GROUPED;
   } else if (a->path == IKL_PATH_MHA_FALLBACK || a->path == IKL_PATH_SCALAR_GROUPED) {
     pl.path = pl.heads_per_kv == 1 ? IKL_PATH_MHA_FALLBACK : a->path;
   } else if (a->path == IKL_PATH_MFMA_GROUPED) {

@@ -426,7 +426,10 @@ def paged_decode_attention_hip_grouped(
         query_group_size=1 if heads_per_kv == 1 else (0 if path_name == "mfma_grouped" else query_group_size),
         partition_size=partition_size,
         max_context_len=max_context_len,
-        path=-1 if cache.fp8 else _PATH_IDS[path_name],  # the FP8 cache is read by the MFMA family only
+        # the FP8 cache is read by the MFMA family only, and partition_size -2
+        # (the balanced split) leaves the family to the library, which runs
+        # it on the MFMA family (MHA included) where that supports the shape
+        path=-1 if cache.fp8 or partition_size == -2 else _PATH_IDS[path_name],
     )
 
 

@@ -125,7 +125,7 @@ def test_split_choice_by_batch_size_on_the_mfma_family():
     a = _args(partition_size=-2, max_context_len=1024, batch=2)
     part = lib.ikl_paged_attention_partition_size(ctypes.byref(a))
     assert part > 0 and part % 16 == 0 and part not in (256, 512)
-    # -2 on the scalar family is refused
+    # -2 where the MFMA family does not run (fp32) is refused
     a = _args(partition_size=-2, max_context_len=1024, dtype=_lib.IKL_F32)
     assert lib.ikl_paged_attention_workspace_size(ctypes.byref(a)) == _lib.IKL_EUNSUPPORTED
     assert "balanced split" in _lib.last_error()
@@ -193,6 +193,9 @@ def test_operators_fail_loudly_without_a_gpu():
         (_lib.IKL_BF16, 4, -1, ("mfma_grouped", 16, 4, "none")),
         (_lib.IKL_F32, 4, 0, ("scalar_grouped", None, 1, "fixed_partitions")),
         (_lib.IKL_F16, 1, 0, ("mha_fallback", None, 1, "fixed_partitions")),
+        # -2 asks for the balanced split, which moves MHA to the MFMA family
+        (_lib.IKL_F16, 1, -2, ("mfma_grouped", 16, 1, "balanced")),
+        (_lib.IKL_BF16, 1, -2, ("mfma_grouped", 16, 1, "balanced")),
     ],
 )
 def test_launch_config_reports_the_resolved_launch(dtype, heads_per_kv, partition, expect):

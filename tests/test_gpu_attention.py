@@ -245,6 +245,29 @@ def test_balanced_split_fewer_tiles_than_waves(lengths):
     _check(case, "paged_decode_attention_hip", label="sk-tiny", partition_size=-2)
 
 
+@pytest.mark.parametrize("dtype,head_dim", [("float16", 128), ("bfloat16", 64)])
+def test_mha_balanced_split_runs_on_the_mfma_family(dtype, head_dim):
+    """partition_size=-2 on MHA (one query head per KV head): the launch
+    moves from the per-head kernel to the MFMA family's balanced split; the
+    plain, grouped and prepared entry points all match the oracle."""
+    from inferkernellab_amd import ops
+
+    gen = np.random.default_rng(50 + head_dim)
+    lengths = [int(x) for x in gen.integers(1, 1500, size=12)]
+    lengths[3] = 1
+    case = make_case(batch=12, num_heads=16, num_kv_heads=16, head_dim=head_dim, block_size=16,
+                     lengths=lengths, dtype=dtype, seed=51)
+    _check(case, "paged_decode_attention_hip", label="mha-sk", partition_size=-2)
+    _check(case, "paged_decode_attention_hip_grouped", label="mha-sk-grouped", partition_size=-2,
+           query_group_size=8)
+    attn = ops.PreparedPagedAttention(case.device_query(), case.device_cache(), case.device_tables(),
+                                      case.device_lengths(), max_context_len=max(lengths), partition_size=-2)
+    assert attn.path == "mfma_grouped" and attn.balanced_split
+    out = attn()
+    torch.cuda.synchronize()
+    assert max_abs_err(out, case.expected()) <= ATOL[dtype]
+
+
 @pytest.mark.parametrize("partition_size", [None, -2, 256])
 def test_empty_contexts_give_nan_rows_and_leave_others_exact(partition_size):
     """validate_inputs=False with zero-length requests: their rows are NaN
