@@ -80,7 +80,20 @@ __global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParam
   const int lane = threadIdx.x;
   const int row = lane / TPT;
   const int sub = lane % TPT;
-  const int part = blockIdx.x;
+  // Grid (partition, unit, request), partition fastest. Consecutive
+  // workgroups are dealt round-robin over the 8 XCDs, so with a multiple of
+  // 8 partitions per request the XCD would be the partition index for every
+  // request, and ragged context lengths would leave the XCDs of the last,
+  // mostly empty partitions idle. The partition index is then rotated by
+  // (unit + request) % 8, which deals each request's partitions over all 8
+  // (MHA 32 hd128 bf16 B32 x U[1024, 4096]: 304 -> 239 us for the whole
+  // operation; fp32 GQA 32/8 B32 x U[1024, 4096]: 158 -> 147 us; uniform
+  // batches unchanged).
+  int part = blockIdx.x;
+  if ((gridDim.x & 7u) == 0u) {
+    part += (int)((blockIdx.y + blockIdx.z) & 7u);
+    if (part >= (int)gridDim.x) part -= (int)gridDim.x;
+  }
   const int kvh = blockIdx.y / p.groups_per_kv;
   const int qg = blockIdx.y % p.groups_per_kv;
   const int64_t b = blockIdx.z;
@@ -539,10 +552,10 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
     // partition_size -2 asks for the balanced split, which the MFMA family
     // runs: an MHA launch left to the library moves there from the per-head
     // kernel when the family supports its shape. On ragged batches the
-    // balanced split beats the per-head kernel's fixed partitions (whole
-    // operation, MALL flushed: MHA 32 hd128 bf16 B32 x U[1024, 4096] 307 ->
-    // 228 us, hd64 fp16 B64 x U[1024, 4096] 303 -> 225 us); on uniform ones
-    // the per-head kernel, which partition_size 0 keeps, is 6-10 % faster.
+    // balanced split is slightly ahead of the per-head kernel's fixed
+    // partitions (whole operation, MALL flushed: MHA 32 hd128 bf16 B32 x
+    // U[1024, 4096] 239 -> 228 us); on uniform ones the per-head kernel,
+    // which partition_size 0 keeps, is 6-10 % faster.
     if (a->partition_size == -2 && pl.path == IKL_PATH_MHA_FALLBACK &&
         mfma_supported(a->dtype, a->head_dim, a->block_size, 1))
       pl.path = IKL_PATH_MFMA_GROUPED;
