@@ -556,9 +556,22 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
     // partitions (whole operation, MALL flushed: MHA 32 hd128 bf16 B32 x
     // U[1024, 4096] 239 -> 228 us); on uniform ones the per-head kernel,
     // which partition_size 0 keeps, is 6-10 % faster.
-    if (a->partition_size == -2 && pl.path == IKL_PATH_MHA_FALLBACK &&
-        mfma_supported(a->dtype, a->head_dim, a->block_size, 1))
-      pl.path = IKL_PATH_MFMA_GROUPED;
+    //
+    // Small MHA launches move there too: with at most 32 MiB of K/V at the
+    // longest context they are latency-bound, and the MFMA kernel's 4-wave
+    // workgroups (a partition's tiles split over 4 waves, merged in LDS)
+    // take fewer dependent steps than the per-head kernel's one wave.
+    // Whole operation, MALL flushed, MHA 32 hd64 fp16: B1 x 128 16.1 ->
+    // 13.6 us, B4 x 128 16.0 -> 13.4, B1 x 512 17.6 -> 15.2, B4 x 512 18.0
+    // -> 17.0, B16 x 128 16.3 -> 15.5; at 64 MiB and above the per-head
+    // kernel is as fast or faster (B16 x 512 25.3 vs 25.6, B4 x 2048 25.6 vs
+    // 27.1, B16 x 2048 62.3 vs 69.8).
+    if (pl.path == IKL_PATH_MHA_FALLBACK && mfma_supported(a->dtype, a->head_dim, a->block_size, 1)) {
+      const int64_t cap_tokens = a->table_width * (int64_t)a->block_size;
+      const int64_t ctx = a->max_context_len > 0 ? std::min<int64_t>(a->max_context_len, cap_tokens) : cap_tokens;
+      const double kv_bytes = (double)a->batch * a->num_kv_heads * ctx * a->head_dim * 2.0 * pl.eb;
+      if (a->partition_size == -2 || kv_bytes <= 32.0 * (1 << 20)) pl.path = IKL_PATH_MFMA_GROUPED;
+    }
   } else if (a->path == IKL_PATH_MHA_FALLBACK || a->path == IKL_PATH_SCALAR_GROUPED) {
     pl.path = pl.heads_per_kv == 1 ? IKL_PATH_MHA_FALLBACK : a->path;
   } else if (a->path == IKL_PATH_MFMA_GROUPED) {

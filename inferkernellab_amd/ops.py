@@ -297,7 +297,9 @@ def launch_config(args) -> dict:
 def _record_launch(args) -> None:
     cfg = launch_config(args)
     _last_launch[cfg["path"]] = cfg
-    if cfg["path"] != "mha_fallback":
+    if args.num_heads == args.num_kv_heads:
+        _last_launch["one_head_per_kv"] = cfg  # whichever family ran it
+    else:
         _last_launch["grouped"] = cfg  # the last launch of either grouped family
 
 
@@ -311,8 +313,10 @@ def paged_decode_autotune_config() -> dict | None:
     (triton_ops.py:17-27 reports the Triton autotuner's pick the same way);
     ``block_n`` = positions per wave loop step, ``num_warps`` = waves per
     workgroup, ``num_stages`` = tiles in flight per wave. None before any
-    launch of that family."""
-    return _reported("mha_fallback")
+    such launch. The library runs small one-head-per-KV-head launches (and
+    any with ``partition_size=-2``) on the matrix-core family; this reports
+    whichever family ran the most recent one."""
+    return _reported("one_head_per_kv")
 
 
 def paged_decode_grouped_autotune_config() -> dict | None:

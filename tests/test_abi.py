@@ -185,6 +185,25 @@ def test_operators_fail_loudly_without_a_gpu():
     assert ops.triton_available is ops.hip_available
 
 
+def test_small_mha_launches_take_the_mfma_family():
+    """One query head per KV head, path left to the library: at most 32 MiB
+    of K/V at the longest context runs on the MFMA family (latency-bound
+    launches), more stays on the per-head kernel; fp32 always does."""
+    lib = _lib.load()
+    small = _args(dtype=_lib.IKL_F16, num_heads=32, num_kv_heads=32, head_dim=64, batch=4, max_context_len=128)
+    assert ops.launch_config(small)["path"] == "mfma_grouped"  # 4 x 32 x 128 x 64 x 2 x 2 B = 4 MiB
+    edge = _args(dtype=_lib.IKL_BF16, num_heads=32, num_kv_heads=32, head_dim=128, batch=4, max_context_len=512)
+    assert ops.launch_config(edge)["path"] == "mfma_grouped"  # exactly 32 MiB
+    big = _args(dtype=_lib.IKL_F16, num_heads=32, num_kv_heads=32, head_dim=64, batch=16, max_context_len=2048)
+    assert ops.launch_config(big)["path"] == "mha_fallback"  # 256 MiB
+    f32 = _args(dtype=_lib.IKL_F32, num_heads=32, num_kv_heads=32, head_dim=64, batch=1, max_context_len=128)
+    assert ops.launch_config(f32)["path"] == "mha_fallback"
+    # an explicit per-head path is kept
+    small.path = _lib.IKL_PATH_MHA_FALLBACK
+    assert ops.launch_config(small)["path"] == "mha_fallback"
+    assert lib.ikl_paged_attention_path(_lib.IKL_F16, 64, 16, 8, 1, 0) == _lib.IKL_PATH_MHA_FALLBACK
+
+
 @pytest.mark.parametrize(
     ("dtype", "heads_per_kv", "partition", "expect"),
     [

@@ -94,9 +94,11 @@ def test_mqa_group_32_bf16():
 
 
 def test_mha_fp16_with_split():
-    case = make_case(batch=4, num_heads=32, num_kv_heads=32, head_dim=128, block_size=16,
-                     lengths=[512] * 4, dtype="float16", seed=32)
-    _check(case, "paged_decode_attention_hip", label="mha", partition_size=128)
+    # 64 MiB of K/V: above the size the library sends to the MFMA family, so
+    # this runs the per-head kernel's split (8 partitions: rotated)
+    case = make_case(batch=8, num_heads=32, num_kv_heads=32, head_dim=128, block_size=16,
+                     lengths=[512] * 8, dtype="float16", seed=32)
+    _check(case, "paged_decode_attention_hip", label="mha", partition_size=64)
 
 
 def test_custom_scale_and_int64_metadata():
