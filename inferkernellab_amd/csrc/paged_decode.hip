@@ -70,14 +70,19 @@ struct ScalarCfg {
   static_assert(TI <= 64, "a tile must fit one table window");
 };
 
-template <typename Tag, int D, int G>
-__global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParams p) {
+// W waves per workgroup share one partition: wave w takes tiles
+// [w n / W, (w + 1) n / W) of its n tiles, and the waves' (m, l, o) merge in
+// LDS before wave 0 writes, so a launch that needs W times the waves of its
+// (partition, unit, request) count gets them without W times the partials.
+template <typename Tag, int D, int G, int W>
+__global__ __launch_bounds__(64 * W) void paged_decode_scalar_kernel(const AttnParams p) {
   using C = ScalarCfg<Tag, D, G>;
   constexpr int TPT = C::TPT, CPL = C::CPL, LD = C::LD, ROWS = C::ROWS, R = C::R, TI = C::TI;
   constexpr int VEC = C::VEC, EB = C::EB;
   constexpr bool F32 = (EB == 4);
 
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = W > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;
   const int row = lane / TPT;
   const int sub = lane % TPT;
   // Grid (partition, unit, request), partition fastest. Consecutive
@@ -102,7 +107,12 @@ __global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParam
   const int64_t part_start = (int64_t)part * p.partition_size;
   if (part > 0 && part_start >= ctx) return;  // no tokens for this partition
   const int64_t part_end = ctx < part_start + p.partition_size ? ctx : part_start + p.partition_size;
-  const int n_tiles = part_end > part_start ? (int)((part_end - part_start + TI - 1) / TI) : 0;
+  const int wg_tiles = part_end > part_start ? (int)((part_end - part_start + TI - 1) / TI) : 0;
+  // this wave's run of the partition's tiles: positions [w_start, w_end)
+  const int t_lo = wave * wg_tiles / W, t_hi = (wave + 1) * wg_tiles / W;
+  const int n_tiles = t_hi - t_lo;
+  const int64_t w_start = part_start + (int64_t)t_lo * TI;
+  const int64_t w_end = part_end < part_start + (int64_t)t_hi * TI ? part_end : part_start + (int64_t)t_hi * TI;
 
   // ---- query heads of this group, kept packed (two halves per word)
   const int head0 = qg * p.group_size;  // index among the kv head's query heads
@@ -138,13 +148,13 @@ __global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParam
   const int lane_off = sub * 16;
 
   // Block-table window: lane j holds table[b, win_base + j] (or -1).
-  int64_t win_base = p.bs_shift >= 0 ? (part_start >> p.bs_shift) : part_start / bs;
+  int64_t win_base = p.bs_shift >= 0 ? (w_start >> p.bs_shift) : w_start / bs;
   int win = load_table_window(p, b, win_base, lane);
 
   // Issues the K/V loads of tile `t` (unconditionally: masked lanes read
   // the zero row) and returns the lane's valid-token mask.
   auto issue_tile = [&](int t, u32x4 (&kr)[R][CPL], u32x4 (&vr)[R][CPL]) -> uint32_t {
-    const int64_t tile_base = part_start + (int64_t)t * TI;
+    const int64_t tile_base = w_start + (int64_t)t * TI;
     const int64_t last = tile_base + TI - 1;
     const int64_t lb_hi = p.bs_shift >= 0 ? (last >> p.bs_shift) : last / bs;
     if (lb_hi >= win_base + 64) {  // wave-uniform: move the window forward
@@ -159,7 +169,7 @@ __global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParam
       const int off = (int)(pos - lb * bs);
       const int idx = (int)(lb - win_base);  // 0..63 by construction of the window
       const int phys = __builtin_amdgcn_ds_bpermute((idx & 63) * 4, win);
-      const bool ok = (pos < part_end) && (phys >= 0);
+      const bool ok = (pos < w_end) && (phys >= 0);
       valid |= (ok ? 1u : 0u) << r;
       const char *krow = ok ? kbase + ((int64_t)phys * p.k_sb + (int64_t)off * p.k_st) * EB : zero_row;
       const char *vrow = ok ? vbase + ((int64_t)phys * p.v_sb + (int64_t)off * p.v_st) * EB : zero_row;
@@ -279,6 +289,51 @@ __global__ __launch_bounds__(64) void paged_decode_scalar_kernel(const AttnParam
       acc[g][i] = a;
     }
     m[g] = mx;
+  }
+
+  // ---- merge the workgroup's waves; wave 0 writes
+  if constexpr (W > 1) {
+    __shared__ float lds_ml[W][2][G];
+    __shared__ float lds_o[W][G][D];
+    if (row == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) lds_o[wave][g][(c * TPT + sub) * VEC + e] = acc[g][c * VEC + e];
+        if (sub == 0) {
+          lds_ml[wave][0][g] = m[g];
+          lds_ml[wave][1][g] = l[g];
+        }
+      }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mx = lds_ml[0][0][g];
+#pragma unroll
+      for (int w = 1; w < W; ++w) mx = fmaxf(mx, lds_ml[w][0][g]);
+      float f[W];
+      float lt = 0.f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        f[w] = fast_exp2(lds_ml[w][0][g] - mx);
+        lt = fmaf(lds_ml[w][1][g], f[w], lt);
+      }
+#pragma unroll
+      for (int c = 0; c < CPL; ++c)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          float a = 0.f;
+#pragma unroll
+          for (int w = 0; w < W; ++w) a = fmaf(lds_o[w][g][(c * TPT + sub) * VEC + e], f[w], a);
+          acc[g][c * VEC + e] = a;
+        }
+      m[g] = mx;
+      l[g] = lt;
+    }
   }
 
   // ---- write: row r writes the heads g with g % ROWS == r
@@ -483,6 +538,7 @@ struct Plan {
   int64_t ws_o_bytes = 0;
   int64_t ws_bytes = 0;
   bool kv_fp8 = false;  // E4M3 cache with per-row scales (MFMA family only)
+  int scalar_waves = 1;  // waves per workgroup of the VALU family (1, 2 or 4)
 };
 
 int elem_bytes(int dtype) {
@@ -656,6 +712,17 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
     // 31.3 -> 29.1 us with 256-token partitions instead of 128)
     const int64_t target = 1024;
     while (P > 128 && units * ((maxctx + P - 1) / P) < target) P /= 2;
+    // When a request needs at most 4 partitions, they become the waves of
+    // one workgroup that merges them in LDS: same waves, no partials and no
+    // reduce launch (MHA fp16 B16 x 512: two 256-token partitions + reduce
+    // -> one 2-wave workgroup per head). With more partitions the split
+    // stays one wave per workgroup: folding 8 into 2 x 4 waves measured
+    // slower on ragged batches (MHA bf16 B32 x 1k-4k: 237 -> 258 us).
+    const int64_t np = (maxctx + P - 1) / P;
+    if (np <= 4) {
+      pl.scalar_waves = np == 1 ? 1 : (np == 2 ? 2 : 4);  // 3 partitions: 4 waves of 3/4 partition each
+      P = maxctx;
+    }
   }
   if (P >= maxctx) {
     pl.split = false;
@@ -680,13 +747,22 @@ void record(void *ev, hipStream_t s) {
   if (ev) (void)hipEventRecord((hipEvent_t)ev, s);
 }
 
-template <typename Tag, int D>
-void launch_scalar(int gmax, const AttnParams &p, dim3 grid, hipStream_t s) {
+template <typename Tag, int D, int W>
+void launch_scalar_waves(int gmax, const AttnParams &p, dim3 grid, hipStream_t s) {
   switch (gmax) {
-    case 1: paged_decode_scalar_kernel<Tag, D, 1><<<grid, 64, 0, s>>>(p); break;
-    case 2: paged_decode_scalar_kernel<Tag, D, 2><<<grid, 64, 0, s>>>(p); break;
-    case 4: paged_decode_scalar_kernel<Tag, D, 4><<<grid, 64, 0, s>>>(p); break;
-    default: paged_decode_scalar_kernel<Tag, D, 8><<<grid, 64, 0, s>>>(p); break;
+    case 1: paged_decode_scalar_kernel<Tag, D, 1, W><<<grid, 64 * W, 0, s>>>(p); break;
+    case 2: paged_decode_scalar_kernel<Tag, D, 2, W><<<grid, 64 * W, 0, s>>>(p); break;
+    case 4: paged_decode_scalar_kernel<Tag, D, 4, W><<<grid, 64 * W, 0, s>>>(p); break;
+    default: paged_decode_scalar_kernel<Tag, D, 8, W><<<grid, 64 * W, 0, s>>>(p); break;
+  }
+}
+
+template <typename Tag, int D>
+void launch_scalar(int gmax, int waves, const AttnParams &p, dim3 grid, hipStream_t s) {
+  switch (waves) {
+    case 2: launch_scalar_waves<Tag, D, 2>(gmax, p, grid, s); break;
+    case 4: launch_scalar_waves<Tag, D, 4>(gmax, p, grid, s); break;
+    default: launch_scalar_waves<Tag, D, 1>(gmax, p, grid, s); break;
   }
 }
 
@@ -703,11 +779,11 @@ void launch_family(int d, const Plan &pl, const AttnParams &p, dim3 grid, hipStr
     return;
   }
   switch (d) {
-    case 16: launch_scalar<Tag, 16>(pl.gmax, p, grid, s); break;
-    case 32: launch_scalar<Tag, 32>(pl.gmax, p, grid, s); break;
-    case 64: launch_scalar<Tag, 64>(pl.gmax, p, grid, s); break;
-    case 96: launch_scalar<Tag, 96>(pl.gmax, p, grid, s); break;
-    default: launch_scalar<Tag, 128>(pl.gmax, p, grid, s); break;
+    case 16: launch_scalar<Tag, 16>(pl.gmax, pl.scalar_waves, p, grid, s); break;
+    case 32: launch_scalar<Tag, 32>(pl.gmax, pl.scalar_waves, p, grid, s); break;
+    case 64: launch_scalar<Tag, 64>(pl.gmax, pl.scalar_waves, p, grid, s); break;
+    case 96: launch_scalar<Tag, 96>(pl.gmax, pl.scalar_waves, p, grid, s); break;
+    default: launch_scalar<Tag, 128>(pl.gmax, pl.scalar_waves, p, grid, s); break;
   }
 }
 
@@ -786,7 +862,7 @@ extern "C" int ikl_paged_attention_launch_config(const ikl_paged_attention_args 
       case IKL_BF16: c.tile_tokens = scalar_tile_tokens_dim<bf16_tag>(a->head_dim, pl.gmax); break;
       default: c.tile_tokens = scalar_tile_tokens_dim<f32_tag>(a->head_dim, pl.gmax); break;
     }
-    c.waves_per_workgroup = 1;
+    c.waves_per_workgroup = pl.scalar_waves;
     c.stages = 2;
   }
   c.split = pl.sk_waves > 0 ? 2 : (pl.split ? 1 : 0);

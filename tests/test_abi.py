@@ -74,13 +74,21 @@ def test_partition_planning_for_the_gqa_decode_shape():
     assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 0
     assert lib.ikl_paged_attention_workspace_size(ctypes.byref(a)) == 0
     # automatic on the scalar family: 512 tokens, halved (down to 128) while
-    # there are fewer than 1024 workgroups (one wave per SIMD of 256 CUs)
+    # there are fewer than 1024 waves (one per SIMD of 256 CUs); when a
+    # request then needs at most 4 partitions they become the waves of one
+    # workgroup and nothing is split
     a = _args(partition_size=0, max_context_len=512, batch=16, num_kv_heads=32, dtype=_lib.IKL_F32)
-    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 256  # 512 units x 2 partitions
+    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 0  # 512 units x 2 waves, no split
+    assert ops.launch_config(a)["num_warps"] == 2
     a = _args(partition_size=0, max_context_len=512, batch=4, num_kv_heads=32, dtype=_lib.IKL_F32)
-    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 128  # the floor
+    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 0  # 128 x 4 covers 512
+    assert ops.launch_config(a)["num_warps"] == 4
     a = _args(partition_size=0, max_context_len=8192, batch=16, num_kv_heads=32, dtype=_lib.IKL_F32)
-    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 512  # 512 x 16 >= 1024 already
+    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 512  # 16 partitions stay split
+    assert ops.launch_config(a)["num_warps"] == 1
+    # an explicit partition size keeps one-wave workgroups
+    a = _args(partition_size=256, max_context_len=8192, batch=16, num_kv_heads=32, dtype=_lib.IKL_F32)
+    assert ops.launch_config(a)["num_warps"] == 1
 
 
 def test_balanced_split_planning_on_the_mfma_family():

@@ -358,6 +358,32 @@ def _fill_by_append(case, ops):
     return cache
 
 
+@pytest.mark.parametrize(
+    ("heads", "kv", "dim", "dtype", "lengths", "waves"),
+    [
+        # MHA fp16, 512 (request, head) units: two 256-token partitions -> 2 waves
+        (32, 32, 128, "float16", [512, 1, 255, 256, 257, 3] + [int(x) for x in
+                                  np.random.default_rng(11).integers(1, 513, size=10)], 2),
+        # fp32 GQA 32/8, 32 units at the 128-token floor: four partitions -> 4 waves
+        (32, 8, 64, "float32", [512, 1, 3, 300], 4),
+        # three 128-token partitions -> 4 waves of 96 tokens
+        (32, 8, 128, "float32", [384, 1, 129, 200], 4),
+    ],
+)
+def test_valu_workgroups_fold_up_to_four_partitions(heads, kv, dim, dtype, lengths, waves):
+    """When a request needs at most 4 partitions on the VALU family, they run
+    as the waves of one workgroup that merges them in LDS (no split, no
+    reduce); ragged and one-token contexts leave some waves without tiles."""
+    from inferkernellab_amd import ops
+
+    case = make_case(batch=len(lengths), num_heads=heads, num_kv_heads=kv, head_dim=dim, block_size=16,
+                     lengths=lengths, dtype=dtype, seed=70 + waves, kv_scale=0.5)
+    fn = "paged_decode_attention_hip" if heads == kv else "paged_decode_attention_hip_grouped"
+    _check(case, fn, label=f"valu-{waves}-waves")
+    cfg = ops.paged_decode_autotune_config() if heads == kv else ops.paged_decode_grouped_autotune_config()
+    assert cfg["num_warps"] == waves
+
+
 def test_config_gqa_fp32_hd64_b4_ctx512():
     """GQA 32/8, head_dim 64, fp32, batch 4 x 512, block 16, 159-block pool,
     scale 1/8; the cache filled by appending every context token."""
