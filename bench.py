@@ -861,7 +861,9 @@ def main() -> int:
     # Correctness gate before timing, like the reference's harness
     # (benchmark.py:225-268, which raises when the kernel differs from its
     # PyTorch reference): one eager step, every request against the oracle.
-    attn()
+    # It runs the timed steps' own launches; the append writes past each
+    # context, where the oracle does not read.
+    run_step()
     torch.cuda.synchronize()
     view = oracle_view(w)
     t_oracle = time.perf_counter()
@@ -873,7 +875,6 @@ def main() -> int:
         print(json.dumps({"error": "decode attention output differs from the oracle", "parity": check}))
         return 3
     checked_out = attn.out.clone()
-    append()
 
     # Eager pass: HIP events recorded around the split kernel and the reduce
     # on their stream (the roofline's kernel time). With the MALL flush, the
@@ -1003,7 +1004,10 @@ def main() -> int:
             "kv_block_layout": "[kv_heads, block_size, D]" if w["cache"].head_major else "[block_size, kv_heads, D]",
             "partition_size": attn.partition_size,
             "split": "balanced (equal tile runs per resident wave)" if attn.balanced_split
-                     else f"fixed partitions of {attn.partition_size} tokens",
+                     else f"fixed partitions of {attn.partition_size} tokens" if attn.launch["split"] != "none"
+                     else ("attention alone: unsplit, up to 4 partitions per request folded into one "
+                           "multi-wave workgroup; the step keeps them split for the reduce to carry the append"
+                           if step.fused else "none"),
             "step": ("paged attention (split kernel + reduce) then 1-token KV append per request: "
                      + ("two operator launches" if args.separate_append or not step.fused
                         else "one library call, the append carried by the reduce kernel")),

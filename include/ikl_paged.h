@@ -330,6 +330,18 @@ int ikl_paged_decode_step(const ikl_paged_attention_args *attention, const ikl_a
 int32_t ikl_paged_decode_step_fused(const ikl_paged_attention_args *attention,
                                     const ikl_append_args *append);
 
+/* Workspace bytes that ikl_paged_decode_step may use with these arguments:
+ * at least ikl_paged_attention_workspace_size. When the attention alone
+ * would run unsplit with a request's partitions folded into one multi-wave
+ * workgroup (the automatic split of the VALU family), the step keeps the
+ * split instead if the append can ride on the reduce and the workspace
+ * holds this many bytes, saving the append's own launch; with a smaller
+ * workspace it runs the folded kernel and then the append. Negative on
+ * invalid arguments. Planning only. No counterpart in the reference (see
+ * ikl_paged_decode_step). */
+int64_t ikl_paged_decode_step_workspace_size(const ikl_paged_attention_args *attention,
+                                             const ikl_append_args *append);
+
 /* Static path selection for a grouped launch; mirrors the role of
  * paged_decode_grouped_path (triton_ops.py:56-75) for this library's
  * kernel families: MHA (heads_per_kv == 1) -> IKL_PATH_MHA_FALLBACK;

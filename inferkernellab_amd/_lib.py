@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "ikl_paged_prefill_path",
     "ikl_paged_decode_step",
     "ikl_paged_decode_step_fused",
+    "ikl_paged_decode_step_workspace_size",
     "ikl_paged_attention_noalloc",
 )
 
@@ -264,6 +265,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ikl_paged_decode_step.argtypes = [ctypes.POINTER(PagedAttentionArgs), ctypes.POINTER(AppendArgs), _c_ptr]
     lib.ikl_paged_decode_step_fused.restype = _c_i32
     lib.ikl_paged_decode_step_fused.argtypes = [ctypes.POINTER(PagedAttentionArgs), ctypes.POINTER(AppendArgs)]
+    lib.ikl_paged_decode_step_workspace_size.restype = _c_i64
+    lib.ikl_paged_decode_step_workspace_size.argtypes = [ctypes.POINTER(PagedAttentionArgs),
+                                                         ctypes.POINTER(AppendArgs)]
     lib.ikl_paged_attention_launch_config.restype = ctypes.c_int
     lib.ikl_paged_attention_launch_config.argtypes = [ctypes.POINTER(PagedAttentionArgs),
                                                       ctypes.POINTER(LaunchConfig)]

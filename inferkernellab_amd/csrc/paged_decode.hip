@@ -572,7 +572,10 @@ int select_path(int dtype, int head_dim, int block_size, int heads_per_kv, int q
   return IKL_PATH_SCALAR_GROUPED;
 }
 
-int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
+// fold_waves: let the automatic VALU split fold up to 4 partitions of a
+// request into one unsplit multi-wave workgroup (false for the decode step's
+// alternative plan, which keeps the split so the reduce carries the append).
+int make_plan(const ikl_paged_attention_args *a, Plan &pl, bool fold_waves = true) {
   if (!a) return fail(IKL_EINVAL, "attention: null argument struct");
   pl.eb = elem_bytes(a->dtype);
   if (!pl.eb) return fail(IKL_EINVAL, "attention: unsupported dtype");
@@ -719,7 +722,7 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl) {
     // stays one wave per workgroup: folding 8 into 2 x 4 waves measured
     // slower on ragged batches (MHA bf16 B32 x 1k-4k: 237 -> 258 us).
     const int64_t np = (maxctx + P - 1) / P;
-    if (np <= 4) {
+    if (fold_waves && np <= 4) {
       pl.scalar_waves = np == 1 ? 1 : (np == 2 ? 2 : 4);  // 3 partitions: 4 waves of 3/4 partition each
       P = maxctx;
     }
@@ -988,12 +991,30 @@ int run_attention(const ikl_paged_attention_args *a, const Plan &pl, const Fused
 
 // Whether a decode step's append rides on the reduce kernel (1), runs as
 // its own launch after the attention (0), or the arguments are invalid (<0).
-int step_plan(const ikl_paged_attention_args *a, const ikl_append_args *app, Plan &pl, FusedAppend &f) {
+// The decode step's plan. When the attention alone would fold a request's
+// partitions into one unsplit VALU workgroup, the step keeps them split if
+// the append can ride on the reduce and the workspace holds the split's
+// partials (ikl_paged_decode_step_workspace_size reports that size): one
+// launch less than the folded kernel followed by the append (MHA fp16
+// B16 x 512: 24.7 + 4.0 us -> 24.0 + 4.0 us by kernel trace, the append
+// costing nothing on the reduce). `alt_ws` receives the split's workspace
+// size, or 0 when no alternative applies.
+int step_plan(const ikl_paged_attention_args *a, const ikl_append_args *app, Plan &pl, FusedAppend &f,
+              int64_t *alt_ws = nullptr) {
   int rc = make_plan(a, pl);
   if (rc != IKL_OK) return rc;
   rc = prepare_fused_append(app, f);
   if (rc < 0) return rc;
-  return rc == IKL_OK && f.rows > 0 && pl.split ? 1 : 0;
+  const bool can_fuse = rc == IKL_OK && f.rows > 0;
+  if (alt_ws) *alt_ws = 0;
+  if (can_fuse && !pl.split && pl.scalar_waves > 1) {
+    Plan alt;
+    if (make_plan(a, alt, false) == IKL_OK && alt.split) {
+      if (alt_ws) *alt_ws = alt.ws_bytes;
+      if (a->workspace && a->workspace_bytes >= alt.ws_bytes && aligned16(a->workspace)) pl = alt;
+    }
+  }
+  return can_fuse && pl.split ? 1 : 0;
 }
 }  // namespace
 }  // namespace ikl
@@ -1063,6 +1084,16 @@ extern "C" int ikl_paged_attention_noalloc(const ikl_paged_attention_args *a, vo
     b.workspace_bytes = (int64_t)IKL_NOALLOC_SCRATCH_BYTES;
   }
   return run_attention(&b, pl, nullptr, stream);
+}
+
+extern "C" int64_t ikl_paged_decode_step_workspace_size(const ikl_paged_attention_args *a,
+                                                        const ikl_append_args *app) {
+  Plan pl;
+  FusedAppend f;
+  int64_t alt = 0;
+  const int mode = step_plan(a, app, pl, f, &alt);
+  if (mode < 0) return mode;
+  return std::max<int64_t>(pl.ws_bytes, alt);
 }
 
 extern "C" int32_t ikl_paged_decode_step_fused(const ikl_paged_attention_args *a, const ikl_append_args *app) {

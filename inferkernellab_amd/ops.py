@@ -630,7 +630,7 @@ class PreparedPagedAttention:
             main = "paged_decode_mfma_streamk_kernel" if self.balanced_split else "paged_decode_mfma_kernel"
         else:
             main = "paged_decode_scalar_kernel"
-        return main, ("paged_decode_reduce_kernel" if self._args.workspace_bytes > 0 else None)
+        return main, ("paged_decode_reduce_kernel" if self.launch["split"] != "none" else None)
 
     def __call__(self, events=None) -> torch.Tensor:
         for i in range(3):
@@ -675,14 +675,25 @@ class PreparedDecodeStep:
     (decode.py:480-487), enqueued by one library call
     (``ikl_paged_decode_step``). When the attention splits, the reduce
     kernel also carries the append — one launch less per step — with the
-    same result as calling the two separately (``fused`` tells which)."""
+    same result as calling the two separately (``fused`` tells which).
+    Where the attention alone would run unsplit on folded multi-wave
+    workgroups, the step keeps the split so that the reduce carries the
+    append; the attention's workspace then grows to the step's size
+    (``ikl_paged_decode_step_workspace_size``)."""
 
     def __init__(self, attention: PreparedPagedAttention, append: PreparedAppend):
         if attention.device != append.device:
             raise ValueError("attention and append must be on the same device")
         self._lib = _require_backend()
         self.attention, self.append = attention, append
-        mode = self._lib.ikl_paged_decode_step_fused(ctypes.byref(attention._args), ctypes.byref(append._args))
+        a, app = ctypes.byref(attention._args), ctypes.byref(append._args)
+        need = self._lib.ikl_paged_decode_step_workspace_size(a, app)
+        _lib.check(need if need < 0 else 0, "decode step")
+        if need > attention._args.workspace_bytes:
+            attention.workspace = torch.empty(need, dtype=torch.uint8, device=attention.device)
+            attention._args.workspace = attention.workspace.data_ptr()
+            attention._args.workspace_bytes = need
+        mode = self._lib.ikl_paged_decode_step_fused(a, app)
         _lib.check(mode if mode < 0 else 0, "decode step")
         self.fused = mode == 1
         self.device = attention.device
@@ -693,8 +704,10 @@ class PreparedDecodeStep:
 
     def kernel_names(self) -> tuple[str, ...]:
         """Kernels one step enqueues, in order."""
-        names = tuple(n for n in self.attention.kernel_names() if n)
-        return names if self.fused else names + ("append_kv_kernel",)
+        main, reduce = self.attention.kernel_names()
+        if self.fused:
+            return main, "paged_decode_reduce_kernel"
+        return tuple(n for n in (main, reduce) if n) + ("append_kv_kernel",)
 
     def __call__(self, events=None) -> torch.Tensor:
         a = self.attention._args
