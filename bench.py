@@ -1016,6 +1016,8 @@ def main() -> int:
             "parallelism": "single GPU",
         },
         "attention_kernel_us": round(kern_avg_ms * 1e3, 2),
+        "attention_kernel_p50_us": round(_percentile(kernel_ms, 0.5) * 1e3, 2),
+        "attention_kernel_p95_us": round(_percentile(kernel_ms, 0.95) * 1e3, 2),
         "reduce_kernel_us": round(sum(reduce_ms) / len(reduce_ms) * 1e3, 2),
         "reduce_carries_append": bool(step.fused and not args.separate_append),
         "algorithmic_bytes_per_step": attn_bytes + append_bytes,

@@ -71,10 +71,10 @@ struct AttnParams {
   // Balanced ("stream-K") split of the MFMA family; sk_waves == 0 selects
   // the fixed partitions above. With sk_waves = W, the global sequence of
   // 16-token tiles — request-major, then (kv head, query group) unit, then
-  // position — is cut into W equal runs, one per wave; the piece of unit s
-  // (= b * units + u) that wave w covers lands in partial slot s + w (the
-  // pairs (s, w) met along the sequence are ordered in both s and w, so the
-  // slots are distinct and each unit's pieces are consecutive).
+  // position — is cut into W equal runs, one per workgroup; the piece of
+  // unit s (= b * units + u) that run w covers lands in partial slot s + w
+  // (the pairs (s, w) met along the sequence are ordered in both s and w, so
+  // the slots are distinct and each unit's pieces are consecutive).
   int32_t sk_waves;
   int32_t units;           // kv heads x query groups per request
   int32_t grid_spread;     // fixed-partition MFMA grid is request-fastest (spread_grid)
@@ -202,14 +202,14 @@ __device__ inline int64_t request_tiles(const AttnParams &p, int64_t b, int lane
   return total;
 }
 
-// The wave of a balanced split over T tiles and W waves (W <= T) whose run
-// [floor(w T / W), floor((w + 1) T / W)) holds global tile g.
+// The run of a balanced split over T tiles and W runs (W <= T),
+// [floor(w T / W), floor((w + 1) T / W)), that holds global tile g.
 __device__ inline int64_t wave_of_tile(int64_t g, int64_t T, int64_t W) { return ((g + 1) * W - 1) / T; }
 
 // MFMA kernel family (paged_decode_mfma.hip). mfma_supported() tells whether
 // a (dtype, head_dim, block_size, group) launch has a compiled MFMA kernel;
 // launch_mfma_attention() enqueues it (grid as for the scalar family, or
-// p.sk_waves one-wave workgroups for the balanced split).
+// p.sk_waves workgroups for the balanced split).
 bool mfma_supported(int dtype, int head_dim, int block_size, int group_size);
 hipError_t launch_mfma_attention(int dtype, int head_dim, const AttnParams &p, dim3 grid, hipStream_t s);
 // Static launch shape of the MFMA family (fixed partitions or balanced split).
@@ -218,8 +218,8 @@ struct MfmaShape {
 };
 MfmaShape mfma_launch_shape(bool balanced, int group_size);
 
-// One-wave workgroups of the balanced-split MFMA kernel (for units of
-// `group_size` heads) resident at once on the current device.
+// Workgroups of the balanced-split MFMA kernel (for units of `group_size`
+// heads) resident at once on the current device.
 int mfma_streamk_capacity(int dtype, int head_dim, int group_size, bool kv_fp8);
 
 }  // namespace ikl

@@ -7,7 +7,8 @@
 // where token p of request b lives at cache[table[b, p / bs], p % bs]
 // (cache.py:113-129, 191-200), like paged_reference (attention.py:134-175).
 //
-// Launch geometry (one wave64 per workgroup):
+// Launch geometry (one wave64 per workgroup; 2 or 4 when up to 4 partitions
+// of a request are folded into one unsplit workgroup):
 //   grid.x = split-context partition (1 when not split)
 //   grid.y = kv_head * groups_per_kv + query_group
 //   grid.z = request
@@ -435,7 +436,7 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(const AttnParam
   int64_t prow, pstride;
   if (p.sk_waves > 0) {
     // balanced split: unit u's pieces sit in consecutive slots s + w for the
-    // waves w whose runs cover its tiles; rows slot * group_size + head.
+    // runs w that cover its tiles; rows slot * group_size + head.
     int64_t before;
     int own;
     const int64_t total = request_tiles(p, b, lane, &before, &own);
@@ -533,7 +534,7 @@ struct Plan {
   int partition = 0;  // tokens per grid.x slot
   int num_parts = 1;
   bool split = false;
-  int sk_waves = 0;  // balanced split (MFMA family): waves sharing the batch's tiles
+  int sk_waves = 0;  // balanced split (MFMA family): runs (workgroups) sharing the batch's tiles
   int64_t units = 0;  // kv heads x query groups per request
   int64_t ws_o_bytes = 0;
   int64_t ws_bytes = 0;
@@ -657,10 +658,10 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl, bool fold_waves = tru
   pl.units = (int64_t)a->num_kv_heads * pl.groups_per_kv;
   const int64_t units = a->batch * pl.units;
 
-  // Balanced split waves: at least SK_MIN_TILES tiles each at the
-  // longest context (a small batch runs fewer, longer waves, not one tile
-  // each; e.g. MQA 32/1 hd64 B16 x 2048: 24.9 -> 16.5 us going from 1 to 4),
-  // capped by the resident capacity.
+  // Balanced split runs (workgroups of SKW waves): at least SK_MIN_TILES
+  // tiles per wave at the longest context (a small batch runs fewer, longer
+  // waves, not one tile each; e.g. MQA 32/1 hd64 B16 x 2048: 24.9 -> 16.5 us
+  // going from 1 to 4), capped by the resident capacity.
   constexpr int64_t SK_MIN_TILES = 4;
   // The balanced split on the MFMA family (one run of ~T/W tiles per
   // resident wave): asked for with partition_size = -2, and picked
@@ -678,11 +679,25 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl, bool fold_waves = tru
   if (a->partition_size == -2 && pl.path != IKL_PATH_MFMA_GROUPED)
     return fail(IKL_EUNSUPPORTED, "partition_size -2 (the balanced split) needs the MFMA kernel family");
   const int64_t t_max = units * ((maxctx + 15) / 16);
+  // 32-head units also take the balanced split as soon as their 512-token
+  // fixed partitions would not fit one round of resident workgroups (the
+  // balanced split's 2-wave runs hold the same resources as the fixed
+  // kernel's 2-wave workgroups). MQA 32/1 hd128 bf16, whole operation: B80 x
+  // U[1024, 4096] (640 workgroups for 512 resident) 46.6 -> 39.4 us, B48 x
+  // U[4096, 8192] 53.2 -> 44.9, B128 54.6 -> 49.1; at or under one round
+  // the fixed partitions stay faster (B64 x U[1024, 4096] 32.8 vs 35.3 us,
+  // B96 x 2048 33.2 vs 39.5).
+  bool past_one_round = false;
+  if (a->partition_size == 0 && pl.path == IKL_PATH_MFMA_GROUPED && pl.group_size > 16)
+    past_one_round = units * ((maxctx + 511) / 512) >
+                     mfma_streamk_capacity(a->dtype, a->head_dim, pl.group_size, pl.kv_fp8);
   const bool want_balanced =
-      a->partition_size == -2 || (a->partition_size == 0 && pl.path == IKL_PATH_MFMA_GROUPED && t_max > SK_MIN_BATCH_TILES);
+      a->partition_size == -2 ||
+      (a->partition_size == 0 && pl.path == IKL_PATH_MFMA_GROUPED && (t_max > SK_MIN_BATCH_TILES || past_one_round));
   if (want_balanced && cap < (int64_t(1) << 29)) {
+    const int64_t skw = mfma_launch_shape(true, pl.group_size).waves_per_workgroup;
     const int64_t w = std::min<int64_t>(mfma_streamk_capacity(a->dtype, a->head_dim, pl.group_size, pl.kv_fp8),
-                                        std::max<int64_t>((t_max + SK_MIN_TILES - 1) / SK_MIN_TILES, 1));
+                                        std::max<int64_t>((t_max + SK_MIN_TILES * skw - 1) / (SK_MIN_TILES * skw), 1));
     if ((double)(t_max + 1) * (double)w < 4.0e18) {
       pl.sk_waves = (int)w;
       pl.split = true;

@@ -22,9 +22,10 @@
 //    waves per (partition, unit, request); its waves split the partition's
 //    tiles and merge their softmax states in LDS before one store;
 //  * balanced split (paged_decode_mfma_streamk_kernel): exactly as many
-//    one-wave workgroups as the GPU holds at once, each taking an equal run
-//    of the batch's global tile sequence (see AttnParams::sk_waves), so every
-//    wave starts once, streams ~T/W tiles and all finish together.
+//    workgroups as the GPU holds at once, each taking an equal run of the
+//    batch's global tile sequence (see AttnParams::sk_waves) and splitting
+//    each piece of it among its waves, so every wave starts once, streams
+//    ~T/W tiles and all finish together.
 //
 // MFMA operand layouts and the transposing LDS read: see mfma_ops.h.
 #include <type_traits>
@@ -583,20 +584,29 @@ __device__ __forceinline__ void sk_next_request(const AttnParams &p, int64_t &b,
   } while (nb == 0);
 }
 
-// Balanced split: one wave per workgroup, p.sk_waves workgroups (grid.x).
-// Wave w attends global tiles [w T / W, (w + 1) T / W) of the batch (T =
-// units x tiles of all requests, W = min(sk_waves, T)) piece by piece — a
-// piece is the part of one (request, unit) inside the run — and writes each
-// piece's normalised output and log2-sum-exp to partial slot unit + w.
-template <typename Tag, int D, int NG, bool KV8>
-__global__ __launch_bounds__(64) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_streamk_kernel(const AttnParams p) {
+// Balanced split: p.sk_waves runs, one workgroup of WAVES waves each
+// (grid.x). Workgroup w attends global tiles [w T / W, (w + 1) T / W) of the
+// batch (T = units x tiles of all requests, W = min(sk_waves, T)) piece by
+// piece — a piece is the part of one (request, unit) inside the run. Its
+// waves take equal (+-1) shares of each piece's tiles and merge them in LDS,
+// as the fixed partitions' workgroups do, and the piece's normalised output
+// and log2-sum-exp go to partial slot unit + w.
+template <typename Tag, int D, int NG, int WAVES, bool KV8>
+__global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_streamk_kernel(const AttnParams p) {
+  static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4, "1, 2 or 4 waves per workgroup");
   using WT = WaveTiles<Tag, D, NG, KV8>;
   constexpr int NH = WT::NH;
+  // LDS: each wave's V tile during a piece; at its end each wave's staged
+  // [NH heads x D] block, which the workgroup sums (separated by barriers).
   constexpr int SLOT = WT::ST_BYTES > WT::VT_BYTES ? WT::ST_BYTES : WT::VT_BYTES;
-  __shared__ __attribute__((aligned(16))) char lds[SLOT];
-  const int lane = threadIdx.x;
+  __shared__ __attribute__((aligned(16))) char lds[WAVES * SLOT];
+  __shared__ float lds_m[WAVES][NH], lds_l[WAVES][NH];
+  const int lane = (int)(threadIdx.x & 63u);
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int64_t U = p.units;
   const int64_t w = blockIdx.x;
+  // every wave computes the same run: the loop below is uniform over the
+  // workgroup, so its barriers are met by all waves
   const SkRun run = sk_run(p, w, lane);
   if (!run.active) return;
   const int64_t g0 = run.g0, g1 = run.g1;
@@ -617,26 +627,59 @@ __global__ __launch_bounds__(64) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_stre
     const int nh = p.group_size < p.heads_per_kv - head0 ? p.group_size : p.heads_per_kv - head0;
     const int64_t hq0 = (int64_t)kvh * p.heads_per_kv + head0;
     const int64_t ctx = clamped_ctx(p, b);
-    const int64_t t_end = t_hi * TILE < ctx ? t_hi * TILE : ctx;
+    // this wave's share of the piece: tiles [a0, a1), positions [a0 * 16, e)
+    const int64_t n = t_hi - t_in;
+    const int64_t a0 = t_in + wave * n / WAVES, a1 = t_in + (wave + 1) * n / WAVES;
+    const int64_t e = a1 * TILE < ctx ? a1 * TILE : ctx;
     wt.load_q(p, b, hq0, nh);
-    wt.attend(p, b, kvh, t_in * TILE, t_end, lds);
+    wt.attend(p, b, kvh, a0 * TILE, a1 > a0 ? e : a0 * TILE, lds + wave * WT::VT_BYTES);
 
-    const int64_t slot = b * U + u + w;
-    float f[NG];
+    // combine the waves: common max M per head, rescaled sums
+    float M[NG], L[NG], f[NG];
 #pragma unroll
-    for (int gi = 0; gi < NG; ++gi) f[gi] = wt.lsum[gi] > 0.f ? 1.f / wt.lsum[gi] : 0.f;
-    __builtin_amdgcn_wave_barrier();
-    wt.stage(stage, f, nh);
-    __builtin_amdgcn_wave_barrier();
-    store_rows_f32<D, NH, 1>(p.part_o + slot * p.group_size * D, stage, nh, lane, 64);
-    if (wt.grp == 0) {
+    for (int gi = 0; gi < NG; ++gi) {
+      M[gi] = wt.m[gi];
+      L[gi] = wt.lsum[gi];
+    }
+    if constexpr (WAVES > 1) {
+      if (wt.grp == 0) {
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+          lds_m[wave][16 * gi + wt.hl] = wt.m[gi];
+          lds_l[wave][16 * gi + wt.hl] = wt.lsum[gi];
+        }
+      }
+      __syncthreads();  // also ends every wave's use of its V tile
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) {
+        const int h = 16 * gi + wt.hl;
+        M[gi] = lds_m[0][h];
+#pragma unroll
+        for (int k = 1; k < WAVES; ++k) M[gi] = fmaxf(M[gi], lds_m[k][h]);
+        L[gi] = 0.f;
+#pragma unroll
+        for (int k = 0; k < WAVES; ++k) L[gi] += lds_l[k][h] * fast_exp2(lds_m[k][h] - M[gi]);
+      }
+    } else {
+      __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi)
+      f[gi] = (WAVES > 1 ? fast_exp2(wt.m[gi] - M[gi]) : 1.f) * (L[gi] > 0.f ? 1.f / L[gi] : 0.f);
+    wt.stage(stage + wave * NH * WT::SROW, f, nh);
+    if constexpr (WAVES > 1) __syncthreads();
+    else __builtin_amdgcn_wave_barrier();
+    const int64_t slot = b * U + u + w;
+    store_rows_f32<D, NH, WAVES>(p.part_o + slot * p.group_size * D, stage, nh, (int)threadIdx.x, 64 * WAVES);
+    if (wave == 0 && wt.grp == 0) {
 #pragma unroll
       for (int gi = 0; gi < NG; ++gi)
         if (16 * gi + wt.hl < nh)
-          p.part_lse[slot * p.group_size + 16 * gi + wt.hl] =
-              wt.lsum[gi] > 0.f ? wt.m[gi] + log2f(wt.lsum[gi]) : -INFINITY;
+          p.part_lse[slot * p.group_size + 16 * gi + wt.hl] = L[gi] > 0.f ? M[gi] + log2f(L[gi]) : -INFINITY;
     }
-    __builtin_amdgcn_wave_barrier();
+    // the staged blocks are read before the next piece's V tiles overwrite them
+    if constexpr (WAVES > 1) __syncthreads();
+    else __builtin_amdgcn_wave_barrier();
 
     g += t_hi - t_in;
     if (g >= g1) break;
@@ -651,10 +694,23 @@ constexpr int wg_waves() {
   return NG == 1 ? 4 : 2;
 }
 
+// Waves per balanced-split workgroup. 32-head units take 2: their pieces'
+// partials are 16 KB each, and merging two waves' shares in LDS halves them
+// (MQA 32/1 hd128 bf16, kernel: B64 x U[1024, 4096] 28.8 -> 27.5 us, B128
+// 41.8 -> 40.3, B32 x U[4096, 8192] 31.0 -> 29.6). 16-head units keep one
+// wave per run: with 4 waves sharing each piece a wave meets more piece
+// starts and barriers, and the GQA 32/8 bf16 B32 x U[4096, 8192] kernel
+// went from 137.7 to 144.1 us.
+template <int NG>
+constexpr int sk_wg_waves() {
+  return NG == 1 ? 1 : 2;
+}
+
 template <typename Tag, int D, int NG, bool KV8>
 void launch_shape(const AttnParams &p, dim3 grid, hipStream_t s) {
   if (p.sk_waves > 0) {
-    paged_decode_mfma_streamk_kernel<Tag, D, NG, KV8><<<dim3((unsigned)p.sk_waves), 64, 0, s>>>(p);
+    constexpr int SKW = sk_wg_waves<NG>();
+    paged_decode_mfma_streamk_kernel<Tag, D, NG, SKW, KV8><<<dim3((unsigned)p.sk_waves), dim3(64 * SKW), 0, s>>>(p);
     return;
   }
   // grid arrives as (partition, unit, request)
@@ -679,14 +735,15 @@ void launch_kv(int d, const AttnParams &p, dim3 grid, hipStream_t s) {
   else launch_dim<Tag, NG, false>(d, p, grid, s);
 }
 
-// Resident one-wave workgroups of the balanced-split kernel on the current
-// device (CUs x workgroups per CU), cached per device; 256 CUs x the
-// kernel's waves per CU (8 for 16-head units, 4 for 32-head) when no device
-// answers (planning on a host without a GPU).
+// Resident workgroups of the balanced-split kernel on the current device
+// (CUs x workgroups per CU), cached per device; 256 CUs x the kernel's
+// waves per CU (8 for 16-head units, 4 for 32-head) / its waves per
+// workgroup when no device answers (planning on a host without a GPU).
 template <typename Tag, int D, int NG, bool KV8>
 int streamk_capacity_for() {
   constexpr int MAX_DEV = 64;
-  constexpr int FALLBACK = 256 * (NG == 1 ? 8 : 4);
+  constexpr int SKW = sk_wg_waves<NG>();
+  constexpr int FALLBACK = 256 * (NG == 1 ? 8 : 4) / SKW;
   static int cache[MAX_DEV] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) {
@@ -696,8 +753,8 @@ int streamk_capacity_for() {
   if (cache[dev] > 0) return cache[dev];
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_mfma_streamk_kernel<Tag, D, NG, KV8>, 64,
-                                                   0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_mfma_streamk_kernel<Tag, D, NG, SKW, KV8>,
+                                                   64 * SKW, 0) != hipSuccess ||
       cus <= 0 || per_cu <= 0) {
     (void)hipGetLastError();
     return FALLBACK;
@@ -742,8 +799,9 @@ hipError_t launch_mfma_attention(int dtype, int head_dim, const AttnParams &p, d
 }
 
 MfmaShape mfma_launch_shape(bool balanced, int group_size) {
-  const int waves = group_size > 16 ? wg_waves<2>() : wg_waves<1>();
-  return MfmaShape{TILE, balanced ? 1 : waves, 2};
+  const int waves = group_size > 16 ? (balanced ? sk_wg_waves<2>() : wg_waves<2>())
+                                    : (balanced ? sk_wg_waves<1>() : wg_waves<1>());
+  return MfmaShape{TILE, waves, 2};
 }
 
 int mfma_streamk_capacity(int dtype, int head_dim, int group_size, bool kv_fp8) {

@@ -93,16 +93,20 @@ def test_partition_planning_for_the_gqa_decode_shape():
 
 def test_balanced_split_planning_on_the_mfma_family():
     """partition_size=0 on bf16 GQA: the balanced split over W resident
-    waves; the workspace holds (units + W) slots of group_size rows."""
+    one-wave workgroups (runs); the workspace holds (units + W) slots of
+    group_size rows."""
     lib = _lib.load()
     a = _args(partition_size=0, max_context_len=8192)
     part = lib.ikl_paged_attention_partition_size(ctypes.byref(a))
     ws = lib.ikl_paged_attention_workspace_size(ctypes.byref(a))
     units, group, tiles = 32 * 8, 4, 32 * 8 * 512
     assert part > 0 and part % 16 == 0
-    waves = -(-tiles // (part // 16))  # lower bound on W from the longest run
-    assert ws >= (units + waves) * group * (128 * 4 + 4)
+    runs = -(-tiles // (part // 16))  # lower bound on W from the longest run
+    assert ws >= (units + runs) * group * (128 * 4 + 4)
+    cfg = ops.launch_config(a)
+    assert (cfg["split"], cfg["num_warps"]) == ("balanced", 1)
     if not torch.cuda.is_available():  # planning without a device assumes 256 CUs x 8 waves
+        assert cfg["workgroups"] == 2048
         assert part == 16 * (tiles // 2048)
         rows = (units + 2048) * group
         assert ws == -(-(rows * 128 * 4) // 256) * 256 + rows * 4
@@ -116,7 +120,7 @@ def test_split_choice_by_batch_size_on_the_mfma_family():
     lib = _lib.load()
     # B32 x 8 kv heads x 8192 tokens: 131072 tiles -> balanced (partition = a wave's run)
     a = _args(partition_size=0, max_context_len=8192)
-    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) not in (256, 512, 0)
+    assert ops.launch_config(a)["split"] == "balanced"
     # B32 x 8 x 1024: 16384 tiles -> fixed 512-token partitions (512 workgroups)
     a = _args(partition_size=0, max_context_len=1024)
     assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 512
@@ -129,10 +133,28 @@ def test_split_choice_by_batch_size_on_the_mfma_family():
     # B32 x 512: one 512-token partition covers the context -> no split
     a = _args(partition_size=0, max_context_len=512)
     assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 0
+    # 32-head units: balanced once 512-token partitions exceed one round of
+    # resident workgroups (512 without a device: 256 CUs x 2 two-wave groups)
+    if not torch.cuda.is_available():
+        a = _args(partition_size=0, max_context_len=4096, batch=64, num_kv_heads=1)  # 512 workgroups
+        assert ops.launch_config(a)["split"] == "fixed_partitions"
+        a = _args(partition_size=0, max_context_len=4096, batch=80, num_kv_heads=1)  # 640
+        assert ops.launch_config(a)["split"] == "balanced"
+        a = _args(partition_size=0, max_context_len=2048, batch=96, num_kv_heads=1)  # 384
+        assert ops.launch_config(a)["split"] == "fixed_partitions"
     # -2: the balanced split on a small batch too
     a = _args(partition_size=-2, max_context_len=1024, batch=2)
     part = lib.ikl_paged_attention_partition_size(ctypes.byref(a))
-    assert part > 0 and part % 16 == 0 and part not in (256, 512)
+    assert part > 0 and part % 16 == 0 and ops.launch_config(a)["split"] == "balanced"
+    # 1024 tiles at the longest context, at least 4 tiles per one-wave run:
+    # 256 runs of 4 tiles
+    assert part == 64 and ops.launch_config(a)["workgroups"] == 256
+    # 32-head units run 2-wave workgroups, at least 4 tiles per wave
+    a = _args(partition_size=-2, max_context_len=4096, batch=64, num_kv_heads=1)
+    cfg = ops.launch_config(a)
+    assert (cfg["split"], cfg["num_warps"]) == ("balanced", 2)
+    if not torch.cuda.is_available():  # 256 CUs x 2 workgroups of 2 waves
+        assert cfg["workgroups"] == 512
     # -2 where the MFMA family does not run (fp32) is refused
     a = _args(partition_size=-2, max_context_len=1024, dtype=_lib.IKL_F32)
     assert lib.ikl_paged_attention_workspace_size(ctypes.byref(a)) == _lib.IKL_EUNSUPPORTED

@@ -193,7 +193,9 @@ def test_repeat_runs_are_bit_identical():
 # ---------------------------------------------------------------- balanced split
 # partition_size=-2 runs the MFMA family's balanced split (None picks it for
 # batches above 32768 tiles): the batch's tiles are cut into one equal run
-# per wave and merged per unit.
+# per workgroup (one wave for units of up to 16 heads; 2 waves for 32-head
+# units, which share each piece of the run and merge it in LDS), and the
+# pieces are merged per unit by the reduce.
 
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 def test_balanced_split_more_than_64_requests(dtype):
@@ -238,6 +240,23 @@ def test_balanced_split_one_unit_across_many_waves():
     case = make_case(batch=1, num_heads=8, num_kv_heads=1, head_dim=128, block_size=32,
                      lengths=[20000], dtype="bfloat16", seed=42)
     _check(case, "paged_decode_attention_hip", label="sk-long", partition_size=-2)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_balanced_split_32_head_units(dtype):
+    """MQA 32/1 hd128: 32-head units run 2-wave workgroups; ragged lengths
+    (one token, one tile, a tile and one token, long) give pieces shorter
+    than a workgroup's waves and pieces spanning several runs."""
+    from inferkernellab_amd import ops
+
+    gen = np.random.default_rng(44)
+    lengths = [int(x) for x in gen.integers(1, 3000, size=9)]
+    lengths[:4] = [1, 16, 17, 4096]
+    case = make_case(batch=len(lengths), num_heads=32, num_kv_heads=1, head_dim=128, block_size=16,
+                     lengths=lengths, dtype=dtype, seed=45, kv_scale=0.5)
+    _check(case, "paged_decode_attention_hip", label="sk-mqa32", partition_size=-2)
+    cfg = ops.paged_decode_grouped_dot_autotune_config()
+    assert cfg["num_warps"] == 2
 
 
 @pytest.mark.parametrize("lengths", [[1], [1, 1, 1], [15, 16, 17, 33]])
@@ -443,7 +462,7 @@ def test_autotune_reporters_describe_the_last_launch():
     ops.paged_decode_attention_hip(case.device_query(), case.device_cache(), case.device_tables(),
                                    case.device_lengths(), partition_size=-2)
     cfg = ops.paged_decode_grouped_dot_autotune_config()
-    assert cfg == {"block_n": 16, "num_warps": 1, "num_stages": 2}  # the balanced split: one-wave groups
+    assert cfg == {"block_n": 16, "num_warps": 1, "num_stages": 2}  # the balanced split: one-wave runs
     case32 = make_case(batch=2, num_heads=8, num_kv_heads=8, head_dim=64, block_size=16,
                        lengths=[30, 40], dtype="float32", seed=51)
     ops.paged_decode_attention_hip(case32.device_query(), case32.device_cache(), case32.device_tables(),
