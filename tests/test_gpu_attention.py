@@ -242,19 +242,21 @@ def test_balanced_split_one_unit_across_many_waves():
     _check(case, "paged_decode_attention_hip", label="sk-long", partition_size=-2)
 
 
-@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
-def test_balanced_split_32_head_units(dtype):
-    """MQA 32/1 hd128: 32-head units run 2-wave workgroups; ragged lengths
-    (one token, one tile, a tile and one token, long) give pieces shorter
-    than a workgroup's waves and pieces spanning several runs."""
+@pytest.mark.parametrize("heads,kv,dim,dtype", [(32, 1, 128, "float16"), (32, 1, 128, "bfloat16"),
+                                                (48, 2, 64, "bfloat16"), (40, 2, 96, "float16")])
+def test_balanced_split_32_head_units(heads, kv, dim, dtype):
+    """Units of 17-32 heads (MQA 32/1, and 24- and 20-head units) run 2-wave
+    workgroups; ragged lengths (one token, one tile, a tile and one token,
+    long) give pieces shorter than a workgroup's waves and pieces spanning
+    several runs."""
     from inferkernellab_amd import ops
 
-    gen = np.random.default_rng(44)
+    gen = np.random.default_rng(44 + heads)
     lengths = [int(x) for x in gen.integers(1, 3000, size=9)]
     lengths[:4] = [1, 16, 17, 4096]
-    case = make_case(batch=len(lengths), num_heads=32, num_kv_heads=1, head_dim=128, block_size=16,
+    case = make_case(batch=len(lengths), num_heads=heads, num_kv_heads=kv, head_dim=dim, block_size=16,
                      lengths=lengths, dtype=dtype, seed=45, kv_scale=0.5)
-    _check(case, "paged_decode_attention_hip", label="sk-mqa32", partition_size=-2)
+    _check(case, "paged_decode_attention_hip", label="sk-32head", partition_size=-2)
     cfg = ops.paged_decode_grouped_dot_autotune_config()
     assert cfg["num_warps"] == 2
 
@@ -387,6 +389,10 @@ def _fill_by_append(case, ops):
         (32, 8, 64, "float32", [512, 1, 3, 300], 4),
         # three 128-token partitions -> 4 waves of 96 tokens
         (32, 8, 128, "float32", [384, 1, 129, 200], 4),
+        # MHA fp32 head_dim 32 (the per-head kernel), 64 units: three partitions -> 4 waves
+        (16, 16, 32, "float32", [384, 1, 100, 250], 4),
+        # MHA bf16 head_dim 16 (no MFMA kernel), two partitions -> 2 waves
+        (16, 16, 16, "bfloat16", [256, 255, 1, 17] * 8, 2),
     ],
 )
 def test_valu_workgroups_fold_up_to_four_partitions(heads, kv, dim, dtype, lengths, waves):
