@@ -115,7 +115,7 @@ constexpr int PWAVES = 4;  // waves per workgroup
 // one; bf16 P is not split into a second MFMA (that cost ~13 % for
 // accuracy the bf16 bound does not need).
 constexpr int PREFILL_NG = 2;
-constexpr int PF = 2;  // tiles fetched ahead
+constexpr int PF = 2;  // tiles held in registers ahead of the one being staged
 #define IKL_PREFILL_WAVES_ATTR __attribute__((amdgpu_waves_per_eu(2, 8)))
 
 // Two E4M3 codes times one fp32 scale -> two 16-bit values (one rounding).
@@ -440,24 +440,38 @@ __global__ __launch_bounds__(64 * PWAVES) IKL_PREFILL_WAVES_ATTR void paged_pref
     }
   };
 
-  // Tile j: registers -> LDS stage j % 2, barrier, refill the registers
-  // with tile j + PF, compute tile j. Stage j % 2 was last read by tile
-  // j - 2, which every wave finished before the barrier of tile j - 1.
-  auto step = [&](int j, Staged &T) {
-    char *kt = lds[j & 1][0];
-    char *vt = lds[j & 1][1];
-    store_tile(T, kt, vt);
-    const uint32_t holes_t = T.holes;
+  // Tile j: store tile j + 1 (held in registers) into LDS stage (j + 1) % 2
+  // and refill those registers with tile j + 1 + PF, compute tile j from
+  // stage j % 2, then one barrier. Stage (j + 1) % 2 last held tile j - 1,
+  // which every wave finished before the barrier ending step j - 1; tile j
+  // was stored in step j - 1 and is visible after that barrier. The stores'
+  // latency thus overlaps the compute instead of preceding the barrier
+  // (8 x 4096 GQA-32/8: 1202-1218 -> 1181-1203 us; the 3k + 1k chunk
+  // 512-558 -> 500-545 us). Even tiles stage through `ta`, odd ones
+  // through `tb`; hol[s] keeps the hole bits of the tile in stage s.
+  static_assert(PF == 2, "a tile and the one it is refilled with share a register set");
+  auto step = [&](int j, Staged &Tn, uint32_t (&hol)[2]) {
+    if (j + 1 < n_tiles) {
+      store_tile(Tn, lds[(j + 1) & 1][0], lds[(j + 1) & 1][1]);
+      hol[(j + 1) & 1] = Tn.holes;
+      if (j + 1 + PF < n_tiles) fetch(j + 1 + PF, Tn);
+    }
+    compute(lds[j & 1][0], lds[j & 1][1], j * PT, hol[j & 1]);
     __syncthreads();
-    if (j + PF < n_tiles) fetch(j + PF, T);
-    compute(kt, vt, j * PT, holes_t);
   };
   Staged ta, tb;
-  if (n_tiles > 0) fetch(0, ta);
-  if (n_tiles > 1) fetch(1, tb);
+  uint32_t hol[2] = {0u, 0u};
+  if (n_tiles > 0) {
+    fetch(0, ta);
+    if (n_tiles > 1) fetch(1, tb);
+    store_tile(ta, lds[0][0], lds[0][1]);
+    hol[0] = ta.holes;
+    if (PF < n_tiles) fetch(PF, ta);
+    __syncthreads();
+  }
   for (int j = 0; j < n_tiles; j += 2) {
-    step(j, ta);
-    if (j + 1 < n_tiles) step(j + 1, tb);
+    step(j, tb, hol);
+    if (j + 1 < n_tiles) step(j + 1, ta, hol);
   }
 
   // Normalise and store. Lane (hl, grp) holds O^T[16 mt + 4 grp + i][row hl].
