@@ -46,8 +46,12 @@ constexpr int pow2_divisor(int n, int cap) {
 constexpr int cmin(int a, int b) { return a < b ? a : b; }
 
 // Lanes per token: at most 8 for groups of <= 4 heads, 16 for groups of 8
-// (more lanes per token keep the per-lane query and accumulator registers
-// of a large group in budget); 16-byte K (and V) loads per lane per tile.
+// and for fp32 4-head groups of 128 dims (more lanes per token keep the
+// per-lane query and accumulator registers of a large group in budget: the
+// fp32 hd128 4-head kernel goes from 256 VGPRs at one wave per SIMD to 172 at
+// two, GQA 32/8 B32 x U[1024, 4096] 149.7 -> 139.9 us; fp32 hd64 4-head
+// groups, 2-head groups and one head stay at 8, where 16 measured slower or
+// equal); 16-byte K (and V) loads per lane per tile.
 constexpr int TPT_CAP_SMALL_GROUP = 8;
 constexpr int TPT_CAP_LARGE_GROUP = 16;
 constexpr int LOADS_PER_LANE = 4;
@@ -59,7 +63,7 @@ struct ScalarCfg {
   static constexpr int NCHUNK = D / VEC;           // chunks per head_dim row
   static_assert(D % VEC == 0, "head_dim must be a multiple of a 16-byte chunk");
   static constexpr int TPT =
-      pow2_divisor(NCHUNK, G >= 8 ? TPT_CAP_LARGE_GROUP : TPT_CAP_SMALL_GROUP);
+      pow2_divisor(NCHUNK, (G >= 8 || (EB == 4 && D >= 128 && G >= 4)) ? TPT_CAP_LARGE_GROUP : TPT_CAP_SMALL_GROUP);
   static constexpr int CPL = NCHUNK / TPT;         // chunks per lane
   static constexpr int LD = CPL * VEC;             // dims per lane
   static constexpr int ROWS = 64 / TPT;            // tokens per row-step
