@@ -17,11 +17,11 @@ def _head_major_copy(case):
     from inferkernellab_amd import PagedKVCache
 
     oc = case.oracle_cache
-    cache = PagedKVCache(oc.num_blocks, oc.block_size, oc.num_kv_heads, oc.head_dim, dtype=torch.bfloat16,
+    cache = PagedKVCache(oc.num_blocks, oc.block_size, oc.num_kv_heads, oc.head_dim, dtype=getattr(torch, case.dtype),
                          device="cuda", head_major=True)
     assert cache.k.stride(3) == oc.block_size * oc.head_dim and cache.k.stride(2) == oc.head_dim
-    cache.k.copy_(storage_to_torch(oc.k, "bfloat16"))
-    cache.v.copy_(storage_to_torch(oc.v, "bfloat16"))
+    cache.k.copy_(storage_to_torch(oc.k, case.dtype))
+    cache.v.copy_(storage_to_torch(oc.v, case.dtype))
     return cache
 
 
@@ -38,6 +38,21 @@ def test_decode_attention_on_head_major_cache(partition, heads, kv):
                                                  case.device_lengths(), partition_size=partition)
     torch.cuda.synchronize()
     assert float(np.max(np.abs(out.float().cpu().numpy() - case.expected()))) < ATOL["bfloat16"]
+
+
+def test_folded_valu_workgroups_on_head_major_cache():
+    """fp32 GQA 32/8: each request's four 128-token partitions run as one
+    4-wave VALU workgroup, reading head-major blocks."""
+    from inferkernellab_amd import ops
+
+    case = make_case(batch=4, num_heads=32, num_kv_heads=8, head_dim=128, block_size=16,
+                     lengths=[512, 1, 300, 129], dtype="float32", seed=77)
+    cache = _head_major_copy(case)
+    out = ops.paged_decode_attention_hip_grouped(case.device_query(), cache, case.device_tables(),
+                                                 case.device_lengths())
+    torch.cuda.synchronize()
+    assert ops.paged_decode_grouped_autotune_config()["num_warps"] == 4
+    assert float(np.max(np.abs(out.float().cpu().numpy() - case.expected()))) < ATOL["float32"]
 
 
 def test_prefill_attention_on_head_major_cache():
