@@ -261,6 +261,17 @@ def test_balanced_split_32_head_units(heads, kv, dim, dtype):
     assert cfg["num_warps"] == 2
 
 
+@pytest.mark.parametrize("batch,lo,hi", [(1, 20000, 20000), (300, 1, 50)])
+def test_balanced_split_32_head_units_extremes(batch, lo, hi):
+    """2-wave runs of 32-head units: one MQA request of 20000 tokens split
+    over every run, and 300 short requests (the in-kernel request scan walks
+    five 64-request chunks; many runs hold several whole requests)."""
+    lengths = [int(x) for x in np.random.default_rng(46).integers(lo, hi + 1, size=batch)]
+    case = make_case(batch=batch, num_heads=32, num_kv_heads=1, head_dim=128, block_size=16,
+                     lengths=lengths, dtype="bfloat16", seed=47, kv_scale=0.5)
+    _check(case, "paged_decode_attention_hip", label="sk-32head-extreme", partition_size=-2)
+
+
 @pytest.mark.parametrize("lengths", [[1], [1, 1, 1], [15, 16, 17, 33]])
 def test_balanced_split_fewer_tiles_than_waves(lengths):
     case = make_case(batch=len(lengths), num_heads=8, num_kv_heads=2, head_dim=64, block_size=16,
