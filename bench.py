@@ -345,31 +345,54 @@ PREFILL_WORKLOADS = {
     "prefill_gqa32x8_hd128_bf16_b8_4k": (8, 32, 8, 128, torch.bfloat16, 0, 4096),
     "prefill_chunk_gqa32x8_hd128_bf16_b8_3k+1k": (8, 32, 8, 128, torch.bfloat16, 3072, 4096),
     "prefill_gqa16x4_hd128_bf16_b8_512": (8, 16, 4, 128, torch.bfloat16, 0, 512),
+    # the 4k prompts over the FP8 (E4M3 + per-row scale) cache
+    "prefill_gqa32x8_hd128_fp8kv_b8_4k": (8, 32, 8, 128, torch.bfloat16, 0, 4096, "fp8"),
 }
 
 
 def build_prefill_workload(name: str, device: torch.device, seed: int = 0):
     from inferkernellab_amd import PagedKVCache
 
-    batch, heads, kv_heads, head_dim, dtype, start, end = PREFILL_WORKLOADS[name]
+    batch, heads, kv_heads, head_dim, dtype, start, end = PREFILL_WORKLOADS[name][:7]
+    fp8 = PREFILL_WORKLOADS[name][7:] == ("fp8",)
     block_size = 16
     gen = torch.Generator().manual_seed(seed)
     need = -(-end // block_size)
     pool = batch * need + 8
     perm = torch.randperm(pool, generator=gen).tolist()
     tables = [perm[b * need : (b + 1) * need] for b in range(batch)]
-    cache = PagedKVCache(pool, block_size, kv_heads, head_dim, dtype=dtype, device=device)
     dgen = torch.Generator(device=device).manual_seed(seed + 1)
-    for t in (cache.k, cache.v):
-        t.normal_(0.0, 1.0, generator=dgen)
+    if fp8:
+        from inferkernellab_amd.cache import quantize_rows_e4m3
+
+        cache = PagedKVCache(pool, block_size, kv_heads, head_dim, dtype=torch.float8_e4m3fn, act_dtype=dtype,
+                             device=device)
+        for codes, scales in ((cache.k, cache.k_scale), (cache.v, cache.v_scale)):
+            for b0 in range(0, pool, 1024):
+                n = min(1024, pool - b0)
+                rows = torch.randn(n, block_size, kv_heads, head_dim, generator=dgen, device=device)
+                c, sc = quantize_rows_e4m3(rows.to(dtype))
+                codes[0, b0 : b0 + n] = c
+                scales[0, b0 : b0 + n] = sc.transpose(1, 2)
+    else:
+        cache = PagedKVCache(pool, block_size, kv_heads, head_dim, dtype=dtype, device=device)
+        for t in (cache.k, cache.v):
+            t.normal_(0.0, 1.0, generator=dgen)
     width = end - start
     query = torch.randn(batch, heads, width, head_dim, generator=dgen, device=device).to(dtype)
     return {
         "cache": cache, "query": query, "tables_list": tables,
         "tables": torch.tensor(tables, dtype=torch.int32, device=device),
         "starts": [start] * batch, "ends": [end] * batch, "dtype": dtype, "heads": heads,
-        "kv_heads": kv_heads, "head_dim": head_dim, "block_size": block_size, "pool": pool,
+        "kv_heads": kv_heads, "head_dim": head_dim, "block_size": block_size, "pool": pool, "fp8": fp8,
     }
+
+
+def dequantized_kv(cache):
+    """(K, V) of an FP8 cache as code x row scale in fp32 (exact), [layers, blocks, block_size, kv_heads, D]."""
+    k = cache.k.float() * cache.k_scale.transpose(2, 3).unsqueeze(-1)
+    v = cache.v.float() * cache.v_scale.transpose(2, 3).unsqueeze(-1)
+    return k, v
 
 
 def prefill_pairs(starts, ends) -> int:
@@ -386,16 +409,25 @@ def prefill_flops(w) -> int:
 def torch_gather_sdpa(w):
     """The reference's prefill path restated on the same GPU (attention.py:289-321):
     gather the whole prefix through the block table, zero the unread slots,
-    build the boolean causal mask and call torch SDPA."""
+    build the boolean causal mask and call torch SDPA. An FP8 cache is read
+    through a dequantized copy in the query dtype (exact: codes carry 4
+    significant bits), made once per workload."""
     import torch.nn.functional as F
 
     cache, q = w["cache"], w["query"]
+    if w.get("fp8"):
+        if "dequantized" not in w:
+            k, v = dequantized_kv(cache)
+            w["dequantized"] = (k.to(q.dtype), v.to(q.dtype))
+        k_all, v_all = w["dequantized"]
+    else:
+        k_all, v_all = cache.k, cache.v
     bs = w["block_size"]
     span = max(w["ends"])
     kpos = torch.arange(span, device=q.device)
     phys = w["tables"].long()[:, kpos // bs]
-    key = cache.k[0][phys, (kpos % bs).unsqueeze(0)]
-    value = cache.v[0][phys, (kpos % bs).unsqueeze(0)]
+    key = k_all[0][phys, (kpos % bs).unsqueeze(0)]
+    value = v_all[0][phys, (kpos % bs).unsqueeze(0)]
     lengths = torch.tensor(w["ends"], device=q.device).view(-1, 1, 1)
     starts = torch.tensor(w["starts"], device=q.device).view(-1, 1, 1)
     key_ok = kpos.view(1, 1, -1) < lengths
@@ -421,7 +453,12 @@ def prefill_oracle_view(w):
         t = t.detach().cpu()
         return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
 
-    return po.OracleCache.wrap(host(w["cache"].k), host(w["cache"].v), dtype), po.to_f32(host(w["query"]), dtype)
+    if w.get("fp8"):  # the FP8 cache is attended dequantised (codes x scales, exact in fp32)
+        k, v = dequantized_kv(w["cache"])
+        oc = po.OracleCache.wrap(k.cpu().numpy(), v.cpu().numpy(), "float32")
+    else:
+        oc = po.OracleCache.wrap(host(w["cache"].k), host(w["cache"].v), dtype)
+    return oc, po.to_f32(host(w["query"]), dtype)
 
 
 def prefill_parity(w, out: torch.Tensor, rows: int = 64) -> dict:
@@ -571,6 +608,7 @@ def run_prefill(args, device) -> int:
             "head_dim": w["head_dim"],
             "block_size": w["block_size"],
             "chunk": [w["starts"][0], w["ends"][0]],
+            "kv_cache": "fp8 e4m3 codes + one fp32 scale per (token, kv head)" if w["fp8"] else "same as dtype",
             "step": "one paged prefill attention launch over the batch's chunks (causal)",
             "parallelism": "single GPU",
         },
