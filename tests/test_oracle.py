@@ -264,6 +264,21 @@ def test_bench_sweep_tables_follow_the_reference_allocation_order(batch, ctx):
     assert {(1, 128): 15, (16, 2048): 2175}.get((batch, ctx), w["pool"]) == w["pool"]
 
 
+def test_bench_fp8_prefill_reference_paths_agree(monkeypatch):
+    """An FP8-cache prefill workload of the bench (E4M3 codes + row scales):
+    its torch gather + masked SDPA over the dequantized cache and the oracle
+    over the same dequantized cache agree within the bf16 bound, so either
+    can check the kernel."""
+    import bench
+
+    monkeypatch.setitem(bench.PREFILL_WORKLOADS, "tiny_fp8", (2, 8, 2, 64, torch.bfloat16, 0, 64, "fp8"))
+    w = bench.build_prefill_workload("tiny_fp8", torch.device("cpu"))
+    assert w["fp8"] and w["cache"].k.dtype == torch.float8_e4m3fn
+    sdpa = bench.torch_gather_sdpa(w).to(torch.bfloat16)
+    check = bench.prefill_parity(w, sdpa, rows=16)
+    assert check["passed"], check
+
+
 def test_bench_sweep_covers_the_published_matrix():
     """Every one of the 54 sweep shapes has its published A100 timings."""
     import bench
