@@ -130,11 +130,13 @@ typedef struct ikl_paged_attention_args {
   /* Query heads that share one K/V tile inside a workgroup: 0 = all heads
    * of a KV head (capped by the kernel family), else 1..heads_per_kv. */
   int32_t query_group_size;
-  /* Tokens per split-context partition: 0 = pick automatically, -1 = never
-   * split (one pass per request), -2 = the balanced split (MFMA family:
-   * equal runs of the batch's tiles per wave; with path -1 an MHA launch
-   * moves to the MFMA family for it where that supports the shape), else a
-   * positive multiple of 64. */
+  /* Tokens per split-context partition: 0 = pick automatically (fixed
+   * partitions or the balanced split; on the VALU family a request needing
+   * at most 4 partitions runs them unsplit as one multi-wave workgroup),
+   * -1 = never split (one pass per request), -2 = the balanced split (MFMA
+   * family: equal runs of the batch's tiles per resident workgroup; with
+   * path -1 an MHA launch moves to the MFMA family for it where that
+   * supports the shape), else a positive multiple of 64. */
   int32_t partition_size;
   /* Host-known upper bound of context_lens (0 = table_width*block_size);
    * only sizes the grid, never read from device memory. Contract: every
