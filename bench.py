@@ -10,7 +10,8 @@ heads, head_dim 128, bf16, block size 16, ragged context lengths uniform in
 [4096, 8192] (seeded), block tables drawn by random permutation from a pool
 of 20,000 physical blocks, K/V/q ~ N(0,1). The split is the library's
 automatic choice (on the MFMA family: the balanced split, one equal run of
-tiles per resident wave, merged by the reduce kernel); ``--partition-size
+tiles per resident workgroup, here one wave each, merged by the reduce
+kernel); ``--partition-size
 512`` selects fixed 512-token partitions instead. Inputs are resident in HBM
 before the timed region.
 
@@ -1041,7 +1042,7 @@ def main() -> int:
             "kv_cache": "fp8 e4m3 codes + one fp32 scale per (token, kv head)" if w["fp8"] else "same as dtype",
             "kv_block_layout": "[kv_heads, block_size, D]" if w["cache"].head_major else "[block_size, kv_heads, D]",
             "partition_size": attn.partition_size,
-            "split": "balanced (equal tile runs per resident wave)" if attn.balanced_split
+            "split": "balanced (equal tile runs per resident workgroup)" if attn.balanced_split
                      else f"fixed partitions of {attn.partition_size} tokens" if attn.launch["split"] != "none"
                      else ("attention alone: unsplit, up to 4 partitions per request folded into one "
                            "multi-wave workgroup; the step keeps them split for the reduce to carry the append"
