@@ -678,22 +678,26 @@ class PreparedDecodeStep:
     same result as calling the two separately (``fused`` tells which).
     Where the attention alone would run unsplit on folded multi-wave
     workgroups, the step keeps the split so that the reduce carries the
-    append; the attention's workspace then grows to the step's size
-    (``ikl_paged_decode_step_workspace_size``)."""
+    append; it then runs on its own copy of the attention's arguments with
+    a workspace of the step's size (``ikl_paged_decode_step_workspace_size``),
+    leaving ``attention`` and anything captured from it untouched."""
 
     def __init__(self, attention: PreparedPagedAttention, append: PreparedAppend):
         if attention.device != append.device:
             raise ValueError("attention and append must be on the same device")
         self._lib = _require_backend()
         self.attention, self.append = attention, append
-        a, app = ctypes.byref(attention._args), ctypes.byref(append._args)
-        need = self._lib.ikl_paged_decode_step_workspace_size(a, app)
+        self._args = attention._args
+        self.workspace = None
+        app = ctypes.byref(append._args)
+        need = self._lib.ikl_paged_decode_step_workspace_size(ctypes.byref(self._args), app)
         _lib.check(need if need < 0 else 0, "decode step")
         if need > attention._args.workspace_bytes:
-            attention.workspace = torch.empty(need, dtype=torch.uint8, device=attention.device)
-            attention._args.workspace = attention.workspace.data_ptr()
-            attention._args.workspace_bytes = need
-        mode = self._lib.ikl_paged_decode_step_fused(a, app)
+            self._args = type(attention._args).from_buffer_copy(attention._args)
+            self.workspace = torch.empty(need, dtype=torch.uint8, device=attention.device)
+            self._args.workspace = self.workspace.data_ptr()
+            self._args.workspace_bytes = need
+        mode = self._lib.ikl_paged_decode_step_fused(ctypes.byref(self._args), app)
         _lib.check(mode if mode < 0 else 0, "decode step")
         self.fused = mode == 1
         self.device = attention.device
@@ -710,7 +714,7 @@ class PreparedDecodeStep:
         return tuple(n for n in (main, reduce) if n) + ("append_kv_kernel",)
 
     def __call__(self, events=None) -> torch.Tensor:
-        a = self.attention._args
+        a = self._args
         for i in range(3):
             a.events[i] = events[i] if events is not None else None
         stream = torch.cuda.current_stream(self.device).cuda_stream

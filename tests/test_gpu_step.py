@@ -101,7 +101,8 @@ def test_step_keeps_the_split_where_the_attention_alone_folds():
     out = step().clone()
     ref = ops.paged_decode_attention_hip(q, ref_cache, tables, lens, partition_size=128, max_context_len=512)
     ops.append_kv_hip(key, value, ref_cache, slots)
-    alone = attn().clone()  # still folded, on the grown workspace
+    assert attn._args.workspace_bytes == 0 and step.workspace is not None  # the step has its own copy
+    alone = attn().clone()  # still folded, without a workspace
     torch.cuda.synchronize()
     assert torch.equal(_bits(out), _bits(ref))
     assert torch.equal(_bits(fused_cache.k), _bits(ref_cache.k))
