@@ -7,7 +7,7 @@ append; attention within tolerance of the oracle, attention.py:134-175)."""
 import pytest
 import torch
 
-from tests.helpers import ATOL, make_case, max_abs_err
+from tests.helpers import ATOL, assert_close_up_to_output_rounding, make_case, max_abs_err
 
 pytestmark = pytest.mark.gpu
 
@@ -186,3 +186,40 @@ def test_step_function_and_graph_replays():
     blk, off = (slots // 16).long(), (slots % 16).long()
     assert torch.equal(cache.k[0][blk, off].view(torch.int16), key.view(torch.int16))
     assert torch.equal(cache.v[0][blk, off].view(torch.int16), value.view(torch.int16))
+
+
+def test_step_on_random_shapes():
+    """30 seeded random decode steps (dtype, heads, head_dim, batch, lengths,
+    split choice): the step's output equals the oracle, and its cache equals
+    a following ikl_append_kv bit for bit, whether the append rides on the
+    reduce or runs on its own (and where the step keeps a split that the
+    attention alone would fold)."""
+    import random
+
+    from inferkernellab_amd import ops
+
+    rng = random.Random(41)
+    for i in range(30):
+        kv = rng.choice([1, 4, 8, 32])
+        heads = rng.choice([h for h in (8, 32) if h % kv == 0])
+        d = rng.choice([64, 128])
+        dtype = rng.choice(["float16", "bfloat16", "float32"])
+        batch = rng.choice([1, 4, 16])
+        maxlen = rng.choice([16, 300, 512, 2000])
+        lengths = [rng.randint(1, maxlen) for _ in range(batch)]
+        kw = rng.choice([{}, {}, {"partition_size": -1}, {"partition_size": 256}, {"max_context_len": maxlen + 16}])
+        if dtype == "float32" and kw.get("partition_size") == -2:
+            kw = {}
+        print(f"random step {i}: B={batch} H={heads} Hkv={kv} D={d} {dtype} max={maxlen} {kw}", flush=True)
+        case, key, value, slots = _step_case(batch=batch, heads=heads, kv=kv, head_dim=d, lengths=lengths,
+                                             dtype=dtype, seed=300 + i)
+        fused_cache, ref_cache = case.device_cache(), case.device_cache()
+        q, tables, lens = case.device_query(), case.device_tables(), case.device_lengths()
+        attn = ops.PreparedPagedAttention(q, fused_cache, tables, lens, **kw)
+        step = ops.PreparedDecodeStep(attn, ops.PreparedAppend(key, value, fused_cache, slots))
+        out = step().clone()
+        ops.append_kv_hip(key, value, ref_cache, slots)
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(fused_cache.k), _bits(ref_cache.k))
+        assert torch.equal(_bits(fused_cache.v), _bits(ref_cache.v))
+        assert_close_up_to_output_rounding(out, case.expected(), dtype)
