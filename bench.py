@@ -794,68 +794,163 @@ def run_sweep(args, device) -> int:
     return 0
 
 
-def main() -> int:
-    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=50)
-    parser.add_argument("--warmup", type=int, default=10)
-    parser.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS))
-    parser.add_argument("--partition-size", type=int, default=None,
-                        help="tokens per fixed split partition (default: the library's automatic split)")
-    parser.add_argument("--cpu-budget-s", type=float, default=15.0)
-    parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--seed", type=int, default=0)
-    parser.add_argument("--kv-layout", choices=("default", "token-major", "head-major"), default="default",
-                        help="cache block layout: [block_size, kv_heads, D] (the reference's, default for "
-                             "16-bit caches) or [kv_heads, block_size, D] (default for the FP8 cache)")
-    parser.add_argument("--separate-append", action="store_true",
-                        help="launch the append as its own kernel after the attention instead of "
-                             "letting the split reduce kernel carry it (same result)")
-    parser.add_argument("--no-graph", action="store_true",
-                        help="time eager launches instead of HIP graph replays of the step")
-    parser.add_argument("--mall-flush", choices=("auto", "on", "off"), default="auto",
-                        help="read a 512 MiB buffer before every timed sample so that the K/V of "
-                             "the step is not served from the 256 MB MALL (auto: when the step's "
-                             "K/V is below 512 MiB, i.e. every workload but the 805 MB GQA one)")
-    parser.add_argument("--copy-calibration", action="store_true",
-                        help="run only a plain 512 MiB device copy (torch copy_) three times: the "
-                             "known-size reference for scaling FETCH_SIZE / WRITE_SIZE counters")
-    parser.add_argument("--sweep", action="store_true",
-                        help="run the reference's 54-shape attention sweep (each shape checked against "
-                             "the oracle, then timed; --steps samples after --warmup launches)")
-    parser.add_argument("--sweep-out", default=None, help="JSONL file for the sweep's per-shape records")
-    args = parser.parse_args()
+# ------------------------------------------------------------------ llama
+LLAMA_E2E_METRIC = "tiny Llama end-to-end paged decode: tokens/s, TPOT ms, bf16"
 
-    if args.gpus != 1:
-        print(json.dumps({"error": "this benchmark runs on exactly one GPU: the paged decode path "
-                                   "is measured on one GPU's share; --gpus must be 1"}))
-        return 2
-    if not torch.cuda.is_available():
-        print(json.dumps({"error": "no GPU visible"}))
-        return 2
 
-    device = torch.device("cuda", 0)
-    torch.cuda.set_device(device)
-    if args.copy_calibration:
-        nbytes = 512 << 20
-        src = torch.ones(nbytes // 4, dtype=torch.int32, device=device)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_calibration": {"bytes_read": nbytes, "bytes_written": nbytes, "launches": 3}}))
-        return 0
+def measure_llama_e2e(device: torch.device, *, check_requests: int, seed: int = 0) -> dict:
+    """The end-to-end configuration: a random-init Llama (8 layers, hidden
+    2048, 16 / 4 heads of 128, intermediate 5632, vocab 32000, RMSNorm, RoPE
+    theta 1e4, seed-0 weights) in bf16; 16 prompts of 512 random ids
+    (seeded), batched prefill under max_num_batched_tokens 4096 (2 batches
+    of 8), then 64 greedy decode steps through the paged runtime (HIP fused
+    RoPE + append, paged prefill and decode kernels, one HIP graph per
+    decode step). A 4-token run warms the kernels and the allocator first;
+    the second run is timed. The first `check_requests` requests are
+    teacher-forced through the CPU oracle (numpy forward rounding to bf16
+    where the bf16 modules round, hf_benchmark.py:764-823's role): greedy
+    agreement, flips with the oracle's margin, and the largest logit error."""
+    import numpy as np
+    from oracle import llama_oracle as lo
 
-    if args.sweep:
-        return run_sweep(args, device)
-    if args.workload in PREFILL_WORKLOADS:
-        return run_prefill(args, device)
+    from inferkernellab_amd.llama import LlamaConfig, LlamaPagedDecodeRunner, random_llama
 
+    cfg = LlamaConfig(vocab_size=32000, hidden_size=2048, intermediate_size=5632, num_hidden_layers=8,
+                      num_attention_heads=16, num_key_value_heads=4, rope_theta=10000.0)
+    model = random_llama(cfg, seed=0, device=device, dtype=torch.bfloat16)
+    gen = torch.Generator().manual_seed(seed)
+    prompts = torch.randint(0, 32000, (16, 512), generator=gen).tolist()
+    kw = dict(block_size=16, max_num_batched_tokens=4096)
+    LlamaPagedDecodeRunner(model, prompts, max_new_tokens=4, **kw).run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    result = LlamaPagedDecodeRunner(model, prompts, max_new_tokens=64, **kw).run()
+    wall_s = time.perf_counter() - t0
+    steps = list(result.decode_step_wall_ms)
+    new_tokens = sum(len(g) for g in result.generated_tokens)
+    decode_s = sum(steps) / 1e3
+    w = lo.weights_from_model(model) if check_requests > 0 else None
+    checked = flips = 0
+    worst, margins = 0.0, []
+    for i in range(min(check_requests, len(prompts))):
+        gen_i = result.generated_tokens[i]
+        ref = lo.teacher_forced_logits(w, cfg, prompts[i], gen_i, round_to="bfloat16")
+        ours = torch.stack([step[i] for step in result.decode_logits]).float().numpy()
+        worst = max(worst, float(np.abs(ours - ref).max()))
+        best = ref.argmax(-1)
+        for j in np.nonzero(np.asarray(gen_i) != best)[0]:
+            flips += 1
+            margins.append(float(ref[j, best[j]] - ref[j, gen_i[j]]))
+        checked += len(gen_i)
+    del w
+    return {
+        "prefill_ms": round(result.prefill_wall_ms, 2),
+        "prefill_batches": result.prefill_batch_count,
+        "prefill_tokens": result.prefill_tokens,
+        "prefill_tokens_per_s": round(result.prefill_tokens / (result.prefill_wall_ms * 1e-3), 1),
+        "ttft_ms": round(result.ttft_wall_ms, 2),
+        "tpot_mean_ms": round(result.tpot_wall_ms, 3),
+        "tpot_p50_ms": round(_percentile(steps, 0.5), 3),
+        "tpot_p95_ms": round(_percentile(steps, 0.95), 3),
+        "decode_tokens_per_s": round(new_tokens / decode_s, 1),
+        "end_to_end_tokens_per_s": round(new_tokens / wall_s, 1),
+        "wall_s": round(wall_s, 3),
+        "generated_tokens": new_tokens,
+        "greedy_checked_tokens": checked,
+        "greedy_agreement": (checked - flips) / checked if checked else None,
+        "greedy_flips": flips,
+        "largest_flip_margin": round(max(margins), 4) if margins else 0.0,
+        "logits_max_abs_err": round(worst, 4),
+        "peak_memory_allocated_bytes": result.peak_memory_allocated_bytes,
+    }
+
+
+def llama_e2e_entry(device: torch.device, *, check_requests: int, seed: int = 0) -> dict:
+    entry = {"spec": "tiny random Llama end-to-end, bf16: 8 layers, hidden 2048, 16 / 4 heads of 128, "
+                     "intermediate 5632, vocab 32000; B16 x 512-token prompts, batched prefill (4096 "
+                     "tokens), 64 greedy decode steps, graph decode"}
+    entry.update(measure_llama_e2e(device, check_requests=check_requests, seed=seed))
+    torch.cuda.empty_cache()
+    return entry
+
+
+def run_llama_e2e(args, device) -> int:
+    t0 = time.perf_counter()
+    e = measure_llama_e2e(device, check_requests=args.check_requests, seed=args.seed)
+    record = {
+        "metric": LLAMA_E2E_METRIC,
+        "value": e["decode_tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": 64,
+        "warmup": 1,
+        "ms_per_step": e["tpot_mean_ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seed-0 random weights, seeded random prompt ids)",
+        "config": {"workload": "llama_e2e", "layers": 8, "hidden": 2048, "num_heads": 16, "num_kv_heads": 4,
+                   "head_dim": 128, "intermediate": 5632, "vocab": 32000, "batch": 16, "prompt_len": 512,
+                   "max_num_batched_tokens": 4096, "new_tokens": 64, "parallelism": "single GPU"},
+        **{k: v for k, v in e.items()},
+        "greedy_criterion": "teacher-forced against the CPU oracle in bf16 rounding; a flip is a token "
+                            "whose oracle logit trails the oracle's argmax by the printed margin",
+    }
+    record["environment"] = environment(sys.argv)
+    record["bench_wall_s"] = round(time.perf_counter() - t0, 1)
+    print(json.dumps(record))
+    return 0
+
+
+# ------------------------------------------------------------------ decode
+class BenchFailure(Exception):
+    """A correctness gate failed: `record` is the JSON line to print."""
+
+    def __init__(self, record: dict):
+        super().__init__(record.get("error", "bench failure"))
+        self.record = record
+
+
+def append_matches(w) -> bool:
+    """Whether the step's 1-token append left exactly the new K/V rows at
+    each request's slot: bit for bit for a 16-bit cache, the codes and
+    scales quantize_rows_e4m3 gives for the FP8 cache."""
+    cache, bs = w["cache"], w["block_size"]
+    slots = w["slots"].long()
+    blk, off = slots // bs, slots % bs
+    if w["fp8"]:
+        from inferkernellab_amd.cache import quantize_rows_e4m3
+
+        ok = True
+        for new, codes, scales in ((w["new_k"], cache.k, cache.k_scale), (w["new_v"], cache.v, cache.v_scale)):
+            c, sc = quantize_rows_e4m3(new)
+            if cache.head_major:
+                got_c = codes[0][blk, :, off]
+            else:
+                got_c = codes[0][blk, off]
+            ok = ok and torch.equal(got_c.view(torch.uint8), c.view(torch.uint8))
+            ok = ok and torch.equal(scales[0][blk, :, off], sc)
+        return bool(ok)
+    views = []
+    for new, t in ((w["new_k"], cache.k), (w["new_v"], cache.v)):
+        got = t[0][blk, :, off] if cache.head_major else t[0][blk, off]
+        views.append(torch.equal(got.view(torch.int16), new.view(torch.int16)))
+    return all(views)
+
+
+def measure_decode(workload: str, device: torch.device, *, steps: int, warmup: int, seed: int = 0,
+                   partition: int | None = None, head_major: bool | None = None, separate_append: bool = False,
+                   graph: bool = True, mall_flush: str = "auto", cpu_budget_s: float | None = None) -> dict:
+    """One decode-step workload, measured: the correctness gate (every
+    request against the oracle, and the appended rows), then `steps` timed
+    steps eagerly with HIP events around the split kernel and the reduce,
+    then as HIP graph replays. Returns the figures (raises BenchFailure when
+    the gate fails)."""
     from inferkernellab_amd import ops
 
-    head_major = {"default": None, "token-major": False, "head-major": True}[args.kv_layout]
-    w = build_workload(args.workload, device, args.seed, head_major=head_major)
-    partition = args.partition_size or WORKLOADS[args.workload][9]
+    w = build_workload(workload, device, seed, head_major=head_major)
+    partition = partition or WORKLOADS[workload][9]
     attn = ops.PreparedPagedAttention(
         w["query"], w["cache"], w["tables"], w["lens"], validate_inputs=True,
         partition_size=partition, max_context_len=max(w["lengths"]),
@@ -865,24 +960,22 @@ def main() -> int:
 
     def run_step(events=None) -> None:
         """Attention then the 1-token append: one library call (the append
-        rides on the split reduce kernel when it can), or with
-        --separate-append the two operators launched one after the other."""
-        if args.separate_append:
+        rides on the split reduce kernel when it can), or, separately, the
+        two operators launched one after the other."""
+        if separate_append:
             attn(events=events)
             append()
         else:
             step(events=events)
 
     events = HipEvents()
-    k_steps, warmup = args.steps, args.warmup
-    ev = [[events.create() for _ in range(3)] for _ in range(k_steps)]
+    ev = [[events.create() for _ in range(3)] for _ in range(steps)]
     attn_bytes, append_bytes = step_bytes(w)
-    flush = args.mall_flush == "on" or (args.mall_flush == "auto" and attn_bytes < (512 << 20))
+    flush = mall_flush == "on" or (mall_flush == "auto" and attn_bytes < (512 << 20))
     flush_buf = MallFlush(device) if flush else None
-
     flush_marks = []
 
-    def flush_mall(i: int) -> None:
+    def flush_mall() -> None:
         """512 MiB of reads (evicts the MALL and the L2s), bracketed by
         events so that the step time can leave it out."""
         if flush_buf is not None:
@@ -899,9 +992,10 @@ def main() -> int:
 
     # Correctness gate before timing, like the reference's harness
     # (benchmark.py:225-268, which raises when the kernel differs from its
-    # PyTorch reference): one eager step, every request against the oracle.
-    # It runs the timed steps' own launches; the append writes past each
-    # context, where the oracle does not read.
+    # PyTorch reference): one eager step, every request against the oracle,
+    # and the appended rows against the new K/V. It runs the timed steps'
+    # own launches; the append writes past each context, where the oracle
+    # does not read, and the timed steps rewrite the same rows.
     run_step()
     torch.cuda.synchronize()
     view = oracle_view(w)
@@ -910,27 +1004,28 @@ def main() -> int:
     first_oracle_s = time.perf_counter() - t_oracle
     check = parity(attn.out, expected, w["dtype"])
     check["checked"] = f"all {len(w['lengths'])} requests x {w['heads']} heads of one eager step"
+    check["append_exact"] = append_matches(w)
     if not check["passed"]:
-        print(json.dumps({"error": "decode attention output differs from the oracle", "parity": check}))
-        return 3
+        raise BenchFailure({"error": "decode attention output differs from the oracle", "workload": workload,
+                            "parity": check})
+    if not check["append_exact"]:
+        raise BenchFailure({"error": "the step's KV append differs from the new rows", "workload": workload,
+                            "parity": check})
     checked_out = attn.out.clone()
+    del expected
 
-    # Eager pass: HIP events recorded around the split kernel and the reduce
-    # on their stream (the roofline's kernel time). With the MALL flush, the
-    # flush runs before each sample, outside the brackets, and its time is
-    # taken out of the wall time.
     for _ in range(warmup):
         run_step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(k_steps):
-        flush_mall(i)
+    for i in range(steps):
+        flush_mall()
         run_step(events=ev[i])
     torch.cuda.synchronize()
     wall_s = eager_wall_s = time.perf_counter() - t0 - flush_seconds()
     step_mode = "eager launches"
     single_graph_us = None
-    if not args.no_graph:
+    if graph:
         # HIP graphs: a decode loop's launch pattern, without the host's
         # per-kernel dispatch. Inside a graph the reduce starts as the split
         # kernel ends, but every replay costs several µs before its first
@@ -957,16 +1052,16 @@ def main() -> int:
             one.replay()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for i in range(k_steps):
-            flush_mall(i)
+        for i in range(steps):
+            flush_mall()
             one.replay()
         torch.cuda.synchronize()
         single_s = time.perf_counter() - t0 - flush_seconds()
-        single_graph_us = single_s * 1e6 / k_steps
+        single_graph_us = single_s * 1e6 / steps
         wall_s = single_s
         step_mode = "hip graph replay, one step per replay"
         if flush_buf is None:
-            many = capture(k_steps)
+            many = capture(steps)
             many.replay()  # warm
             torch.cuda.synchronize()
             t0 = time.perf_counter()
@@ -975,55 +1070,99 @@ def main() -> int:
             wall_s = time.perf_counter() - t0
             step_mode = "hip graph of the K steps back to back, replayed once"
             del many
+        del one
     torch.cuda.synchronize()
     # every timed step recomputes the checked output (same inputs; the
     # append writes past each context): the last one must equal it bit for bit
-    check["timed_steps_equal_checked_step"] = bool(torch.equal(attn.out.view(torch.int16) if attn.out.element_size() == 2
-                                                               else attn.out, checked_out.view(torch.int16)
-                                                               if checked_out.element_size() == 2 else checked_out))
-    if not check["timed_steps_equal_checked_step"]:
-        print(json.dumps({"error": "timed steps changed the attention output", "parity": check}))
-        return 3
+    same = torch.equal(attn.out.view(torch.int16) if attn.out.element_size() == 2 else attn.out,
+                       checked_out.view(torch.int16) if checked_out.element_size() == 2 else checked_out)
+    check["timed_steps_equal_checked_step"] = bool(same)
+    if not same:
+        raise BenchFailure({"error": "timed steps changed the attention output", "workload": workload,
+                            "parity": check})
     kernel_ms = [events.elapsed_ms(e[0], e[1]) for e in ev]
     reduce_ms = [events.elapsed_ms(e[1], e[2]) for e in ev]
+    both_ms = [events.elapsed_ms(e[0], e[2]) for e in ev]
     for trio in ev:
         for h in trio:
             events.destroy(h)
 
-    ms_per_step = wall_s * 1e3 / k_steps
-    step_gbps = (attn_bytes + append_bytes) / (ms_per_step * 1e-3) / 1e9
-    kern_avg_ms = sum(kernel_ms) / len(kernel_ms)
-    # Algorithmic bytes of the partition kernel: K/V + q + tables + lengths
-    # (+ its fp32 partial writes are workspace traffic, not algorithmic).
-    achieved = attn_bytes / (kern_avg_ms * 1e-3) / 1e9
-
     traffic = None
-    traffic_file = ROOT / "profiles" / f"traffic_{args.workload}.json"
+    traffic_file = ROOT / "profiles" / f"traffic_{workload}.json"
     if traffic_file.exists():
         try:
             traffic = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
+    cpu = cpu_baseline(w, view, cpu_budget_s, first_oracle_s) if cpu_budget_s is not None else None
+    kern_avg_ms = sum(kernel_ms) / len(kernel_ms)
+    m = {
+        "workload": workload,
+        "w": {k: w[k] for k in ("lengths", "dtype", "fp8", "heads", "kv_heads", "head_dim", "block_size", "pool")},
+        "head_major": w["cache"].head_major,
+        "attn": attn,
+        "step": step,
+        "separate_append": separate_append,
+        "flush": flush,
+        "steps": steps,
+        "warmup": warmup,
+        "wall_s": wall_s,
+        "eager_wall_s": eager_wall_s,
+        "single_graph_us": single_graph_us,
+        "step_mode": step_mode,
+        "kernel_ms": kernel_ms,
+        "reduce_ms": reduce_ms,
+        "both_ms": both_ms,
+        "kern_avg_ms": kern_avg_ms,
+        "attn_bytes": attn_bytes,
+        "append_bytes": append_bytes,
+        "check": check,
+        "traffic": traffic,
+        "cpu": cpu,
+        "mfma": mfma_figures(w, attn, kern_avg_ms, workload),
+    }
+    del w, view
+    return m
 
-    cpu = None
-    if not args.no_cpu_baseline:
-        cpu = cpu_baseline(w, view, args.cpu_budget_s, first_oracle_s)
 
-    record = {
+def split_name(m) -> str:
+    attn, step = m["attn"], m["step"]
+    if attn.balanced_split:
+        return "balanced (equal tile runs per resident workgroup)"
+    if attn.launch["split"] != "none":
+        return f"fixed partitions of {attn.partition_size} tokens"
+    if step.fused:
+        return ("attention alone: unsplit, up to 4 partitions per request folded into one multi-wave "
+                "workgroup; the step keeps them split for the reduce to carry the append")
+    return "none"
+
+
+def decode_record(m) -> dict:
+    """The headline JSON record of one measured decode workload."""
+    w, attn, step = m["w"], m["attn"], m["step"]
+    k_steps = m["steps"]
+    ms_per_step = m["wall_s"] * 1e3 / k_steps
+    step_gbps = (m["attn_bytes"] + m["append_bytes"]) / (ms_per_step * 1e-3) / 1e9
+    kern_avg_ms = m["kern_avg_ms"]
+    # Algorithmic bytes of the partition kernel: K/V + q + tables + lengths
+    # (+ its fp32 partial writes are workspace traffic, not algorithmic).
+    achieved = m["attn_bytes"] / (kern_avg_ms * 1e-3) / 1e9
+    return {
         "metric": METRIC,
         "value": round(step_gbps, 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": k_steps,
-        "warmup": warmup,
+        "warmup": m["warmup"],
         "ms_per_step": round(ms_per_step, 4),
         "us_per_step": round(ms_per_step * 1e3, 1),
-        "step_mode": step_mode,
+        "step_mode": m["step_mode"],
         "step_timing": ("wall clock around the K steps, synchronized on both sides, minus the "
-                        "event-timed 512 MiB MALL flush read before each step" if flush
+                        "event-timed 512 MiB MALL flush read before each step" if m["flush"]
                         else "wall clock around the K steps, synchronized on both sides"),
-        "eager_us_per_step": round(eager_wall_s * 1e6 / k_steps, 1),
-        "one_step_graph_us_per_step": round(single_graph_us, 1) if single_graph_us is not None else None,
+        "eager_us_per_step": round(m["eager_wall_s"] * 1e6 / k_steps, 1),
+        "one_step_graph_us_per_step": (round(m["single_graph_us"], 1) if m["single_graph_us"] is not None
+                                       else None),
         "pct_of_peak_hbm": round(100 * step_gbps / PEAK_HBM_GBPS, 1),
         "higher_is_better": True,
         "scaling": "weak",
@@ -1031,7 +1170,7 @@ def main() -> int:
         "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[w["dtype"]],
         "data": "synthetic (seeded N(0,1) K/V/q, random-permutation block tables)",
         "config": {
-            "workload": args.workload,
+            "workload": m["workload"],
             "batch": len(w["lengths"]),
             "num_heads": w["heads"],
             "num_kv_heads": w["kv_heads"],
@@ -1040,40 +1179,348 @@ def main() -> int:
             "num_blocks": w["pool"],
             "context_tokens": sum(w["lengths"]),
             "kv_cache": "fp8 e4m3 codes + one fp32 scale per (token, kv head)" if w["fp8"] else "same as dtype",
-            "kv_block_layout": "[kv_heads, block_size, D]" if w["cache"].head_major else "[block_size, kv_heads, D]",
+            "kv_block_layout": "[kv_heads, block_size, D]" if m["head_major"] else "[block_size, kv_heads, D]",
             "partition_size": attn.partition_size,
-            "split": "balanced (equal tile runs per resident workgroup)" if attn.balanced_split
-                     else f"fixed partitions of {attn.partition_size} tokens" if attn.launch["split"] != "none"
-                     else ("attention alone: unsplit, up to 4 partitions per request folded into one "
-                           "multi-wave workgroup; the step keeps them split for the reduce to carry the append"
-                           if step.fused else "none"),
+            "split": split_name(m),
             "step": ("paged attention (split kernel + reduce) then 1-token KV append per request: "
-                     + ("two operator launches" if args.separate_append or not step.fused
+                     + ("two operator launches" if m["separate_append"] or not step.fused
                         else "one library call, the append carried by the reduce kernel")),
-            "kernels": ([n for n in attn.kernel_names() if n] + ["append_kv_kernel"] if args.separate_append
+            "kernels": ([n for n in attn.kernel_names() if n] + ["append_kv_kernel"] if m["separate_append"]
                         else list(step.kernel_names())),
             "parallelism": "single GPU",
         },
         "attention_kernel_us": round(kern_avg_ms * 1e3, 2),
-        "attention_kernel_p50_us": round(_percentile(kernel_ms, 0.5) * 1e3, 2),
-        "attention_kernel_p95_us": round(_percentile(kernel_ms, 0.95) * 1e3, 2),
-        "reduce_kernel_us": round(sum(reduce_ms) / len(reduce_ms) * 1e3, 2),
-        "reduce_carries_append": bool(step.fused and not args.separate_append),
-        "algorithmic_bytes_per_step": attn_bytes + append_bytes,
+        "attention_kernel_p50_us": round(_percentile(m["kernel_ms"], 0.5) * 1e3, 2),
+        "attention_kernel_p95_us": round(_percentile(m["kernel_ms"], 0.95) * 1e3, 2),
+        "reduce_kernel_us": round(sum(m["reduce_ms"]) / len(m["reduce_ms"]) * 1e3, 2),
+        "reduce_carries_append": bool(step.fused and not m["separate_append"]),
+        "algorithmic_bytes_per_step": m["attn_bytes"] + m["append_bytes"],
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
-            "traffic": traffic,
+            "traffic": m["traffic"],
             "kernel": attn.kernel_names()[0],
-            "algorithmic_bytes_per_launch": attn_bytes,
+            "algorithmic_bytes_per_launch": m["attn_bytes"],
         },
-        "mfma": mfma_figures(w, attn, kern_avg_ms, args.workload),
-        "parity": check,
-        "cpu_baseline": cpu,
+        "mfma": m["mfma"],
+        "parity": m["check"],
+        "cpu_baseline": m["cpu"],
     }
+
+
+def config_entry(m, spec: str) -> dict:
+    """One measured decode workload, compact, for the default line's
+    `configs` block: parity, kernel / reduce / step times and the kernel's
+    roofline fraction."""
+    rec = decode_record(m)
+    kernel_us = rec["attention_kernel_us"]
+    both_us = sum(m["both_ms"]) / len(m["both_ms"]) * 1e3
+    step_bytes_ = m["attn_bytes"] + m["append_bytes"]
+    return {
+        "spec": spec,
+        "workload": m["workload"],
+        "dtype": rec["dtype"],
+        "kv_cache": rec["config"]["kv_cache"],
+        "split": rec["config"]["split"],
+        "partition_size": rec["config"]["partition_size"],
+        "step": rec["config"]["step"],
+        "kernels": rec["config"]["kernels"],
+        "max_abs_err": m["check"]["max_abs_err"],
+        "tolerance": m["check"]["tolerance"],
+        "parity_passed": m["check"]["passed"],
+        "append_exact": m["check"]["append_exact"],
+        "kernel_us": kernel_us,
+        "kernel_p50_us": rec["attention_kernel_p50_us"],
+        "reduce_us": rec["reduce_kernel_us"],
+        "kernel_plus_reduce_us": round(both_us, 2),
+        "step_us": rec["us_per_step"],
+        "step_mode": rec["step_mode"],
+        "mall_flushed": m["flush"],
+        "algorithmic_bytes_per_launch": m["attn_bytes"],
+        "algorithmic_bytes_per_step": step_bytes_,
+        "roofline_frac": rec["roofline"]["frac"],
+        "kernel_plus_reduce_frac": round(step_bytes_ / (both_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
+        "step_frac": round(rec["pct_of_peak_hbm"] / 100, 4),
+    }
+
+
+def c1_cpu_reference(device: torch.device, samples: int = 10, warmup: int = 2) -> dict:
+    """The CPU decode configuration: batch 4, context 512, GQA 32 / 8, head_dim
+    64, fp32, block 16, 159 physical blocks. q, k and v come from seed 0 in
+    the order the reference's case builder draws them (benchmark.py:73-110:
+    per request a key then a value tensor, then the query); each request's
+    table is a slice of one random permutation (seed 1) of the 159 blocks;
+    the cache is filled by appending every context token through
+    slot_mapping (the oracle's write_slots, cache.py:156-189, and the HIP
+    append into the device cache, compared bit for bit). The oracle's
+    paged_reference is timed over `samples` whole steps after `warmup`
+    (BASELINE: warmup plus at least 10 samples); the HIP kernel runs on the
+    same inputs beside it."""
+    import numpy as np
+    from oracle import paged_oracle as po
+
+    from inferkernellab_amd import PagedKVCache, ops
+
+    B, L, H, HKV, D, BS, NB = 4, 512, 32, 8, 64, 16, 159
+    gen_state = torch.random.get_rng_state()
+    torch.manual_seed(0)
+    keys, values = [], []
+    for _ in range(B):
+        k = torch.randn(L, HKV, D, dtype=torch.float32)
+        keys.append(k)
+        values.append(torch.randn_like(k))
+    query = torch.randn(B, H, D, dtype=torch.float32)
+    torch.random.set_rng_state(gen_state)
+    perm = torch.randperm(NB, generator=torch.Generator().manual_seed(1)).tolist()
+    per = L // BS
+    tables = [perm[b * per:(b + 1) * per] for b in range(B)]
+    oc = po.OracleCache(NB, BS, HKV, D, dtype="float32", fill=np.nan)
+    slots = [oc.slot_mapping(t, 0, L) for t in tables]
+    for b in range(B):
+        oc.write_slots(0, slots[b], keys[b].numpy(), values[b].numpy())
+    q = query.numpy()
+    times = []
+    for i in range(warmup + samples):
+        t0 = time.perf_counter()
+        expected = po.paged_decode_attention(q, oc, tables, [L] * B)
+        if i >= warmup:
+            times.append(time.perf_counter() - t0)
+    mean_s = sum(times) / len(times)
+    kv_bytes = B * L * HKV * D * 2 * 4
+
+    # the HIP path on the same inputs: append every token, then attend
+    cache = PagedKVCache(NB, BS, HKV, D, dtype=torch.float32, device=device)
+    cache.k.fill_(float("nan"))
+    cache.v.fill_(float("nan"))
+    dev_slots = torch.tensor(np.concatenate(slots), dtype=torch.int32, device=device)
+    ops.append_kv_hip(torch.cat(keys).to(device), torch.cat(values).to(device), cache, dev_slots)
+    torch.cuda.synchronize()
+    append_exact = bool(np.array_equal(cache.k.cpu().numpy(), oc.k, equal_nan=True)
+                        and np.array_equal(cache.v.cpu().numpy(), oc.v, equal_nan=True))
+    tables_d = torch.tensor(tables, dtype=torch.int32, device=device)
+    lens_d = torch.full((B,), L, dtype=torch.int32, device=device)
+    attn = ops.PreparedPagedAttention(query.to(device), cache, tables_d, lens_d, max_context_len=L)
+    attn()
+    torch.cuda.synchronize()
+    err = float(np.max(np.abs(attn.out.cpu().numpy() - expected)))
+    for _ in range(5):
+        attn()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(20):
+        attn()
+    stop.record()
+    stop.synchronize()
+    hip_us = start.elapsed_time(stop) * 1e3 / 20
+    return {
+        "spec": "CPU paged_reference decode attention, fp32: B4 x ctx 512, GQA 32/8, head_dim 64, block 16, "
+                "159 blocks; seed-0 q/k/v, seed-1 permutation tables, cache filled by append",
+        "cpu_paged_reference_us": round(mean_s * 1e6, 1),
+        "cpu_p50_us": round(_percentile(times, 0.5) * 1e6, 1),
+        "cpu_p95_us": round(_percentile(times, 0.95) * 1e6, 1),
+        "cpu_gbps": round(kv_bytes / mean_s / 1e9, 3),
+        "samples": samples,
+        "warmup": warmup,
+        "cores": host_threads(),
+        "kind": "port",
+        "cpu_sample": "oracle paged_reference (numpy fp32 per-request loop), whole steps of all 4 requests",
+        "hip_append_exact": append_exact,
+        "hip_kernel_us": round(hip_us, 2),
+        "hip_path": attn.path,
+        "hip_max_abs_err": err,
+        "tolerance": TOLERANCE[torch.float32],
+        "hip_parity_passed": bool(err <= TOLERANCE[torch.float32]),
+    }
+
+
+def read_ceiling(device: torch.device, nbytes: int = 512 << 20, samples: int = 5) -> dict:
+    """Event-timed plain-stream read of a contiguous 512 MiB buffer
+    (ikl_hbm_read_probe), best and median of `samples` launches after one
+    warm launch: the HBM read rate the device delivers in this run."""
+    from inferkernellab_amd import _lib
+
+    lib = _lib.load()
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device=device)
+    sink = torch.zeros(1 << 14, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+
+    def launch():
+        _lib.check(lib.ikl_hbm_read_probe(ctypes.c_void_p(buf.data_ptr()), nbytes, ctypes.c_void_p(sink.data_ptr()),
+                                          sink.numel() * 4, ctypes.c_void_p(stream)), "read probe")
+
+    launch()
+    times = []
+    for _ in range(samples):
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        launch()
+        stop.record()
+        stop.synchronize()
+        times.append(start.elapsed_time(stop) * 1e-3)
+    best = min(times)
+    med = sorted(times)[len(times) // 2]
+    del buf
+    return {
+        "read_ceiling_gbps": round(nbytes / best / 1e9, 1),
+        "read_median_gbps": round(nbytes / med / 1e9, 1),
+        "bytes": nbytes,
+        "samples": samples,
+        "kernel": "hbm_read_probe_kernel (16-byte non-temporal loads, 8 workgroups of 256 per CU)",
+    }
+
+
+def environment(argv) -> dict:
+    """Where and from what the line was measured (the reference records
+    its environment beside every result: benchmark.py:154-163,
+    hf_benchmark.py:847-871)."""
+    import hashlib
+    import platform
+
+    from inferkernellab_amd import _lib
+    from inferkernellab_amd.build import source_hash
+
+    props = torch.cuda.get_device_properties(0)
+    lib = _lib.load()
+    version = lib.ikl_version().decode()
+    so_hash = hashlib.sha256(_lib.LIB_PATH.read_bytes()).hexdigest()[:16]
+    built = dict(part.split(":", 1) for part in version.split()[-1].split(",") if ":" in part)
+    rocm = None
+    try:
+        rocm = Path("/opt/rocm/.info/version").read_text().strip()
+    except OSError:
+        pass
+    return {
+        "gpu": props.name,
+        "gcn_arch": getattr(props, "gcnArchName", None),
+        "compute_units": props.multi_processor_count,
+        "hbm_bytes": props.total_memory,
+        "torch": torch.__version__,
+        "hip": torch.version.hip,
+        "rocm": rocm,
+        "library": version,
+        "library_sha256_16": so_hash,
+        "library_abi_version": lib.ikl_abi_version(),
+        "built_from_git": built.get("git"),
+        "built_source_hash": built.get("src"),
+        "library_matches_sources": built.get("src") == source_hash(),
+        "host_cpu": cpu_model(),
+        "host_logical_cpus": os.cpu_count(),
+        "python": platform.python_version(),
+        "command": " ".join([Path(sys.executable).name, *argv]),
+    }
+
+
+# The default line's configurations beyond the headline: (key, workload,
+# partition, spec). The fixed-512 entry is the GQA configuration exactly as
+# written (512-token partitions + reduce), beside the automatic split the
+# headline times.
+DEFAULT_CONFIGS = (
+    ("mha_fp16_append", "mha32_hd128_fp16_b16_ctx512", None,
+     "MHA paged decode + KV append, fp16: B16 x 512, 32 = 32 heads, head_dim 128, block 16"),
+    ("mqa_bf16", "mqa32x1_hd128_bf16_b64_ctx1k-4k", None,
+     "MQA paged decode, bf16: B64, 32 / 1 heads, head_dim 128, ragged U[1024, 4096], K/V 0.5 N(0,1)"),
+    ("gqa_bf16_fixed512", DEFAULT_WORKLOAD, 512,
+     "GQA 32/8 hd128 bf16 B32 x U[4096, 8192] with split-context partitions of 512 tokens + reduce"),
+    ("gqa_fp8kv", "gqa32x8_hd128_fp8kv_b32_ctx4k-8k", None,
+     "the GQA decode configuration over the FP8 (E4M3, per-row scale) KV cache"),
+)
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--workload", default=DEFAULT_WORKLOAD,
+                        choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS) + ["llama_e2e"])
+    parser.add_argument("--partition-size", type=int, default=None,
+                        help="tokens per fixed split partition (default: the library's automatic split)")
+    parser.add_argument("--cpu-budget-s", type=float, default=15.0)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-configs", action="store_true",
+                        help="the headline workload only: no configs block, read ceiling or CPU decode case")
+    parser.add_argument("--seed", type=int, default=0)
+    parser.add_argument("--kv-layout", choices=("default", "token-major", "head-major"), default="default",
+                        help="cache block layout: [block_size, kv_heads, D] (the reference's, default for "
+                             "16-bit caches) or [kv_heads, block_size, D] (default for the FP8 cache)")
+    parser.add_argument("--separate-append", action="store_true",
+                        help="launch the append as its own kernel after the attention instead of "
+                             "letting the split reduce kernel carry it (same result)")
+    parser.add_argument("--no-graph", action="store_true",
+                        help="time eager launches instead of HIP graph replays of the step")
+    parser.add_argument("--mall-flush", choices=("auto", "on", "off"), default="auto",
+                        help="read a 512 MiB buffer before every timed sample so that the K/V of "
+                             "the step is not served from the 256 MB MALL (auto: when the step's "
+                             "K/V is below 512 MiB, i.e. every workload but the 805 MB GQA one)")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="run only a plain 512 MiB device copy (torch copy_) three times: the "
+                             "known-size reference for scaling FETCH_SIZE / WRITE_SIZE counters")
+    parser.add_argument("--sweep", action="store_true",
+                        help="run the reference's 54-shape attention sweep (each shape checked against "
+                             "the oracle, then timed; --steps samples after --warmup launches)")
+    parser.add_argument("--sweep-out", default=None, help="JSONL file for the sweep's per-shape records")
+    parser.add_argument("--check-requests", type=int, default=16,
+                        help="llama_e2e: requests whose greedy tokens are checked against the CPU oracle")
+    args = parser.parse_args()
+
+    if args.gpus != 1:
+        print(json.dumps({"error": "this benchmark runs on exactly one GPU: the paged decode path "
+                                   "is measured on one GPU's share; --gpus must be 1"}))
+        return 2
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        return 2
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    if args.copy_calibration:
+        nbytes = 512 << 20
+        src = torch.ones(nbytes // 4, dtype=torch.int32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration": {"bytes_read": nbytes, "bytes_written": nbytes, "launches": 3}}))
+        return 0
+
+    if args.sweep:
+        return run_sweep(args, device)
+    if args.workload in PREFILL_WORKLOADS:
+        return run_prefill(args, device)
+    if args.workload == "llama_e2e":
+        return run_llama_e2e(args, device)
+
+    t_start = time.perf_counter()
+    head_major = {"default": None, "token-major": False, "head-major": True}[args.kv_layout]
+    try:
+        m = measure_decode(args.workload, device, steps=args.steps, warmup=args.warmup, seed=args.seed,
+                           partition=args.partition_size, head_major=head_major,
+                           separate_append=args.separate_append, graph=not args.no_graph,
+                           mall_flush=args.mall_flush,
+                           cpu_budget_s=None if args.no_cpu_baseline else args.cpu_budget_s)
+        record = decode_record(m)
+        del m
+        if args.workload == DEFAULT_WORKLOAD and not args.no_configs:
+            configs = {"cpu_decode_fp32": c1_cpu_reference(device)}
+            for key, workload, partition, spec in DEFAULT_CONFIGS:
+                cm = measure_decode(workload, device, steps=args.steps, warmup=args.warmup, seed=args.seed,
+                                    partition=partition, graph=not args.no_graph, mall_flush=args.mall_flush)
+                configs[key] = config_entry(cm, spec)
+                del cm
+                torch.cuda.empty_cache()
+            configs["llama_e2e"] = llama_e2e_entry(device, check_requests=2, seed=args.seed)
+            record["configs"] = configs
+            record["read_ceiling"] = read_ceiling(device)
+            record["roofline"]["frac_of_read_ceiling"] = round(
+                record["roofline"]["achieved"] / record["read_ceiling"]["read_ceiling_gbps"], 4)
+    except BenchFailure as exc:
+        print(json.dumps(exc.record))
+        return 3
+    record["environment"] = environment(sys.argv)
+    record["bench_wall_s"] = round(time.perf_counter() - t_start, 1)
     print(json.dumps(record))
     return 0
 

@@ -278,6 +278,23 @@ const char *ikl_last_error(void);
 /* Library version string. */
 const char *ikl_version(void);
 
+/* Reads `bytes` of a contiguous device buffer once (16-byte aligned, a
+ * multiple of 16 bytes) with streaming vector loads, and writes nothing of
+ * note: `sink` (sink_bytes >= 4 x 8 x CU count) only receives a word in the
+ * case its loads XOR to a fixed tag, which keeps them from being optimised
+ * away. Timing it on a buffer larger than the MALL states the plain-stream
+ * HBM read rate of the device, the ceiling for the attention kernels'
+ * algorithmic GB/s. A measurement aid with no counterpart in the
+ * reference. */
+int ikl_hbm_read_probe(const void *buffer, int64_t bytes, void *sink, int64_t sink_bytes, void *stream);
+
+/* Version of this C ABI (the argument structs and entry points declared
+ * here). A caller compares it with IKL_ABI_VERSION of the header it was
+ * built against and refuses to run on a mismatch. No counterpart in the
+ * reference, whose operators are Python functions. */
+#define IKL_ABI_VERSION 3
+int32_t ikl_abi_version(void);
+
 /* KV append (in place). Slots outside [0, num_blocks*block_size) are skipped,
  * never written. Replaces append.py:69-106 / cache.py:156-189. */
 int ikl_append_kv(const ikl_append_args *args, void *stream);
@@ -304,7 +321,10 @@ int ikl_paged_attention(const ikl_paged_attention_args *args, void *stream);
  * hipGetSymbolAddress, on the first call with that device current). No
  * counterpart in the reference: for callers that cannot allocate (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). args->workspace / workspace_bytes are ignored. A launch whose
+ * hipMalloc). The first call on each device must run outside stream
+ * capture: it looks the array's address up with hipGetSymbolAddress; later
+ * calls only enqueue kernels and may be captured.
+ * args->workspace / workspace_bytes are ignored. A launch whose
  * split needs more than IKL_NOALLOC_SCRATCH_BYTES (see
  * ikl_paged_attention_workspace_size) fails with IKL_EWORKSPACE. All calls
  * on one device share the array: calls that overlap on that device (on
@@ -346,7 +366,18 @@ int64_t ikl_paged_decode_step_workspace_size(const ikl_paged_attention_args *att
 
 /* Static path selection for a grouped launch; mirrors the role of
  * paged_decode_grouped_path (triton_ops.py:56-75) for this library's
- * kernel families: MHA (heads_per_kv == 1) -> IKL_PATH_MHA_FALLBACK;
+ * kernel families. Name mapping to the reference's strings:
+ * IKL_PATH_MHA_FALLBACK = "mha_fallback" and IKL_PATH_SCALAR_GROUPED =
+ * "scalar_grouped" in both; IKL_PATH_MFMA_GROUPED ("mfma_grouped" in the
+ * Python wrapper) is the counterpart of the reference's
+ * "tensorcore_short_context" (the dense group x tile contraction on the
+ * matrix cores). The two rules differ where the reference's kernel has
+ * limits this one does not: the reference answers "scalar_grouped" for
+ * table_width > 16 or an effective group below 4 heads, where this library
+ * still runs the matrix cores, and it takes any head_dim >= 16 where this
+ * one needs 32, 64, 96 or 128; the other rows of the reference's truth
+ * table (tests/test_attention.py:22-42) agree under the mapping.
+ * Rule: MHA (heads_per_kv == 1) -> IKL_PATH_MHA_FALLBACK;
  * fp16/bf16 with head_dim in {32, 64, 96, 128} and block_size a multiple of
  * 16 -> IKL_PATH_MFMA_GROUPED; otherwise IKL_PATH_SCALAR_GROUPED. The
  * reference's selector has no block_size argument; this one needs it
@@ -358,8 +389,12 @@ int32_t ikl_paged_attention_path(int32_t dtype, int32_t head_dim, int32_t block_
                                  int32_t query_group_size);
 
 /* Resolved launch of an ikl_paged_attention call (filled by
- * ikl_paged_attention_launch_config). */
+ * ikl_paged_attention_launch_config). The caller sets struct_size to
+ * sizeof(ikl_launch_config) of the header it was built against; the library
+ * fills only the fields that fit in it, so the struct can grow at its end
+ * without older callers being written past. */
 typedef struct ikl_launch_config {
+  int32_t struct_size;         /* in: bytes the caller allocated (>= IKL_LAUNCH_CONFIG_MIN_BYTES) */
   int32_t path;                /* enum ikl_attention_path */
   int32_t tile_tokens;         /* positions one wave takes per loop step */
   int32_t waves_per_workgroup;
@@ -370,11 +405,16 @@ typedef struct ikl_launch_config {
   int32_t group_size;          /* query heads that share each K/V tile (one unit) */
 } ikl_launch_config;
 
+/* Smallest struct_size accepted: the struct up to and including `workgroups`
+ * (group_size and later fields are filled when struct_size covers them). */
+#define IKL_LAUNCH_CONFIG_MIN_BYTES 40
+
 /* Launch configuration `args` resolves to, without launching. Replaces the
  * autotune-config reporters of triton_ops.py:17-53 (block_n / num_warps /
  * num_stages of the last autotuned launch): these kernels are not
  * autotuned, their configuration follows from the arguments. Returns 0 or
- * a negative IKL_E* code. */
+ * a negative IKL_E* code (IKL_EINVAL when out->struct_size is below
+ * IKL_LAUNCH_CONFIG_MIN_BYTES). */
 int ikl_paged_attention_launch_config(const ikl_paged_attention_args *args, ikl_launch_config *out);
 
 #ifdef __cplusplus

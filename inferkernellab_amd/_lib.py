@@ -22,10 +22,14 @@ IKL_F16, IKL_BF16, IKL_F32, IKL_FP8_E4M3 = 0, 1, 2, 3
 IKL_I32, IKL_I64 = 0, 1
 IKL_OK, IKL_EINVAL, IKL_EUNSUPPORTED, IKL_ELAUNCH, IKL_EWORKSPACE = 0, -1, -2, -3, -4
 IKL_PATH_MHA_FALLBACK, IKL_PATH_SCALAR_GROUPED, IKL_PATH_MFMA_GROUPED = 0, 1, 2
+# IKL_ABI_VERSION of the header these mirrors follow; load() refuses a
+# library that reports another
+IKL_ABI_VERSION = 3
 
 EXPORTED_SYMBOLS = (
     "ikl_last_error",
     "ikl_version",
+    "ikl_abi_version",
     "ikl_append_kv",
     "ikl_paged_attention_workspace_size",
     "ikl_paged_attention_partition_size",
@@ -39,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "ikl_paged_decode_step_fused",
     "ikl_paged_decode_step_workspace_size",
     "ikl_paged_attention_noalloc",
+    "ikl_hbm_read_probe",
 )
 
 _c_i64 = ctypes.c_int64
@@ -222,6 +227,7 @@ class LaunchConfig(ctypes.Structure):
     """Mirror of ikl_launch_config."""
 
     _fields_ = [
+        ("struct_size", _c_i32),
         ("path", _c_i32),
         ("tile_tokens", _c_i32),
         ("waves_per_workgroup", _c_i32),
@@ -243,6 +249,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ikl_last_error.argtypes = []
     lib.ikl_version.restype = ctypes.c_char_p
     lib.ikl_version.argtypes = []
+    lib.ikl_abi_version.restype = _c_i32
+    lib.ikl_abi_version.argtypes = []
     lib.ikl_append_kv.restype = ctypes.c_int
     lib.ikl_append_kv.argtypes = [ctypes.POINTER(AppendArgs), _c_ptr]
     lib.ikl_paged_attention_workspace_size.restype = _c_i64
@@ -268,6 +276,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ikl_paged_decode_step_workspace_size.restype = _c_i64
     lib.ikl_paged_decode_step_workspace_size.argtypes = [ctypes.POINTER(PagedAttentionArgs),
                                                          ctypes.POINTER(AppendArgs)]
+    lib.ikl_hbm_read_probe.restype = ctypes.c_int
+    lib.ikl_hbm_read_probe.argtypes = [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]
     lib.ikl_paged_attention_launch_config.restype = ctypes.c_int
     lib.ikl_paged_attention_launch_config.argtypes = [ctypes.POINTER(PagedAttentionArgs),
                                                       ctypes.POINTER(LaunchConfig)]
@@ -290,6 +300,11 @@ def load() -> ctypes.CDLL:
             _load_error = f"cannot load {LIB_PATH}: {exc}"
             raise RuntimeError(_load_error) from exc
         _declare(lib)
+        version = lib.ikl_abi_version()
+        if version != IKL_ABI_VERSION:
+            _load_error = (f"{LIB_PATH.name} implements C ABI version {version}, these bindings "
+                           f"version {IKL_ABI_VERSION}; rebuild with `python -m inferkernellab_amd.build`")
+            raise RuntimeError(_load_error)
         _lib = lib
         return lib
 

@@ -28,6 +28,7 @@ SOURCES = (
     "paged_decode_mfma.hip",
     "paged_prefill.hip",
     "rope_append.hip",
+    "read_probe.hip",
 )
 
 COMMON_FLAGS = [
@@ -58,6 +59,40 @@ SOURCE_FLAGS = {
 }
 
 
+def source_hash() -> str:
+    """First 16 hex digits of a SHA-256 over the kernel sources and the C
+    ABI header (names and contents, sorted): the library embeds it, so a
+    run can tell whether the library it loaded was built from the sources
+    beside it."""
+    import hashlib
+
+    h = hashlib.sha256()
+    files = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h")) + [PACKAGE_DIR.parent / "include" / "ikl_paged.h"]
+    for f in files:
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def build_info() -> str:
+    """'src:<source hash>,git:<revision>[-dirty]' (no spaces: it travels as a
+    preprocessor definition)."""
+    rev = "unknown"
+    try:
+        root = PACKAGE_DIR.parent
+        out = subprocess.run(["git", "rev-parse", "--short=12", "HEAD"], cwd=root, capture_output=True,
+                             text=True, timeout=10)
+        if out.returncode == 0:
+            rev = out.stdout.strip()
+            st = subprocess.run(["git", "status", "--porcelain", "--untracked-files=no"], cwd=root,
+                                capture_output=True, text=True, timeout=10)
+            if st.returncode == 0 and st.stdout.strip():
+                rev += "-dirty"
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return f"src:{source_hash()},git:{rev}"
+
+
 def _hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(path).exists():
@@ -79,9 +114,11 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
     BUILD_DIR.mkdir(exist_ok=True)
     objs = [BUILD_DIR / (name.replace(".hip", ".o")) for name in SOURCES]
     jobs = min(len(SOURCES), max(1, os.cpu_count() or 1))
+    info = [f'-DIKL_BUILD_INFO="{build_info()}"']
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
         futures = [
-            pool.submit(_compile, hipcc, CSRC / name, obj, [*SOURCE_FLAGS.get(name, []), *extra])
+            pool.submit(_compile, hipcc, CSRC / name, obj,
+                        [*SOURCE_FLAGS.get(name, []), *(info if name == "abi.hip" else []), *extra])
             for name, obj in zip(SOURCES, objs)
         ]
         for future in futures:

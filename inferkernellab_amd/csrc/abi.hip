@@ -25,4 +25,13 @@ int check_launch(const char *what) {
 
 extern "C" const char *ikl_last_error(void) { return ikl::g_last_error.c_str(); }
 
-extern "C" const char *ikl_version(void) { return "ikl_paged 0.1 gfx950"; }
+// Build provenance, set by the build: a hash of the kernel sources and the
+// header, and the git revision they were built from (+ "-dirty" when the
+// working tree differed from it).
+#ifndef IKL_BUILD_INFO
+#define IKL_BUILD_INFO "src:unknown,git:unknown"
+#endif
+
+extern "C" const char *ikl_version(void) { return "ikl_paged 0.1 gfx950 " IKL_BUILD_INFO; }
+
+extern "C" int32_t ikl_abi_version(void) { return IKL_ABI_VERSION; }

@@ -28,6 +28,8 @@
 #include <math.h>
 
 #include <algorithm>
+#include <cstddef>
+#include <cstring>
 #include <mutex>
 #include <string>
 
@@ -877,8 +879,15 @@ int scalar_tile_tokens_dim(int d, int gmax) {
 }  // namespace
 }  // namespace ikl
 
+static_assert(offsetof(ikl_launch_config, group_size) == IKL_LAUNCH_CONFIG_MIN_BYTES,
+              "IKL_LAUNCH_CONFIG_MIN_BYTES ends at the first field added after the first version");
+
 extern "C" int ikl_paged_attention_launch_config(const ikl_paged_attention_args *a, ikl_launch_config *out) {
   if (!out) return fail(IKL_EINVAL, "launch config: null output struct");
+  if (out->struct_size < IKL_LAUNCH_CONFIG_MIN_BYTES)
+    return fail(IKL_EINVAL, "launch config: struct_size " + std::to_string(out->struct_size) +
+                                " is below the " + std::to_string(IKL_LAUNCH_CONFIG_MIN_BYTES) +
+                                " bytes of the smallest ikl_launch_config");
   Plan pl;
   int rc = make_plan(a, pl);
   if (rc != IKL_OK) return rc;
@@ -903,7 +912,10 @@ extern "C" int ikl_paged_attention_launch_config(const ikl_paged_attention_args 
   c.workgroups = pl.sk_waves > 0 ? (int64_t)pl.sk_waves
                                  : (int64_t)pl.num_parts * a->num_kv_heads * pl.groups_per_kv * a->batch;
   c.group_size = pl.group_size;
-  *out = c;
+  // fill what the caller's struct holds (an older, shorter struct keeps its size)
+  const size_t n = std::min<size_t>((size_t)out->struct_size, sizeof(c));
+  c.struct_size = out->struct_size;
+  std::memcpy(out, &c, n);
   return IKL_OK;
 }
 

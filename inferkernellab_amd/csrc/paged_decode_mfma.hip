@@ -28,6 +28,7 @@
 //    ~T/W tiles and all finish together.
 //
 // MFMA operand layouts and the transposing LDS read: see mfma_ops.h.
+#include <atomic>
 #include <type_traits>
 
 #include "ikl_common.h"
@@ -183,6 +184,10 @@ struct WaveTiles {
     const int n_tiles = t1 > t0 ? (int)((t1 - t0 + TILE - 1) / TILE) : 0;
     const char *kbase = p.kc + (int64_t)kvh * p.k_sh * CEB;
     const char *vbase = p.vc + (int64_t)kvh * p.v_sh * CEB;
+    // KV8: the head's scale rows, in 64 bits (kvh * head stride may pass 4 GiB)
+    const int64_t shead = KV8 ? (int64_t)kvh * p.s_sh * 4 : 0;
+    const char *ksbase = KV8 ? (const char *)p.k_scale + shead : nullptr;
+    const char *vsbase = KV8 ? (const char *)p.v_scale + shead : nullptr;
     // byte strides: blocks (< 2^32, checked by the host) and token rows
     const uint32_t kblk = (uint32_t)(p.k_sb * CEB), vblk = (uint32_t)(p.v_sb * CEB);
     const uint32_t kst = (uint32_t)(p.k_st * CEB), vst = (uint32_t)(p.v_st * CEB);
@@ -228,12 +233,12 @@ struct WaveTiles {
         }
         // scales of tokens 4 grp .. +3 of the tile's block (16 bytes; a
         // masked block reads zero)
-        const uint64_t so = (uint64_t)pu * (uint32_t)(p.s_sb * 4) + (uint32_t)(kvh * p.s_sh * 4) + off * 4;
+        const uint64_t so = (uint64_t)pu * (uint32_t)(p.s_sb * 4) + off * 4;
         const int sn = nv > 0 ? 64 : 0;
         const __amdgpu_buffer_rsrc_t ksr =
-            __builtin_amdgcn_make_buffer_rsrc((void *)((const char *)p.k_scale + so), (short)0, sn, 0x00020000);
+            __builtin_amdgcn_make_buffer_rsrc((void *)(ksbase + so), (short)0, sn, 0x00020000);
         const __amdgpu_buffer_rsrc_t vsr =
-            __builtin_amdgcn_make_buffer_rsrc((void *)((const char *)p.v_scale + so), (short)0, sn, 0x00020000);
+            __builtin_amdgcn_make_buffer_rsrc((void *)(vsbase + so), (short)0, sn, 0x00020000);
         T.ks = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ksr, 16 * grp, 0, CPOL_NT));
         T.vs = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vsr, 16 * grp, 0, CPOL_NT));
       } else {
@@ -744,13 +749,16 @@ int streamk_capacity_for() {
   constexpr int MAX_DEV = 64;
   constexpr int SKW = sk_wg_waves<NG>();
   constexpr int FALLBACK = 256 * (NG == 1 ? 8 : 4) / SKW;
-  static int cache[MAX_DEV] = {0};
+  // Written once per device by whichever thread gets there first; every
+  // writer stores the same value, and readers see 0 (query again) or it.
+  static std::atomic<int> cache[MAX_DEV] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) {
     (void)hipGetLastError();
     return FALLBACK;
   }
-  if (cache[dev] > 0) return cache[dev];
+  const int known = cache[dev].load(std::memory_order_acquire);
+  if (known > 0) return known;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_mfma_streamk_kernel<Tag, D, NG, SKW, KV8>,
@@ -759,8 +767,8 @@ int streamk_capacity_for() {
     (void)hipGetLastError();
     return FALLBACK;
   }
-  cache[dev] = cus * per_cu;
-  return cache[dev];
+  cache[dev].store(cus * per_cu, std::memory_order_release);
+  return cus * per_cu;
 }
 
 template <typename Tag, int NG, bool KV8>

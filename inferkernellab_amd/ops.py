@@ -63,6 +63,15 @@ def _require_backend() -> ctypes.CDLL:
         raise RuntimeError(f"HIP paged-decode backend is unavailable: {exc}") from exc
 
 
+# Kernel family names of paged_decode_grouped_path -> the reference's names
+# for the corresponding kernel (triton_ops.py:56-75).
+REFERENCE_PATH_NAMES = {
+    "mha_fallback": "mha_fallback",
+    "mfma_grouped": "tensorcore_short_context",
+    "scalar_grouped": "scalar_grouped",
+}
+
+
 def paged_decode_grouped_path(
     *,
     dtype: torch.dtype,
@@ -82,6 +91,12 @@ def paged_decode_grouped_path(
     (keyword, default 16 like the reference's caches) is an addition the
     MFMA tiles need. The library's ``ikl_paged_attention_path`` applies the
     same rule.
+
+    ``"mfma_grouped"`` is this library's counterpart of the reference's
+    ``"tensorcore_short_context"`` (``REFERENCE_PATH_NAMES`` maps each
+    name); the reference picks it only for table_width <= 16 and groups of
+    at least 4 heads, and answers ``"scalar_grouped"`` elsewhere, where the
+    matrix cores here still run.
     """
     if heads_per_kv == 1:
         return "mha_fallback"
@@ -281,6 +296,7 @@ def launch_config(args) -> dict:
     only: needs the library, not a GPU)."""
     lib = _lib.load()
     out = _lib.LaunchConfig()
+    out.struct_size = ctypes.sizeof(out)
     _lib.check(lib.ikl_paged_attention_launch_config(ctypes.byref(args), ctypes.byref(out)), "launch config")
     return {
         "path": _PATH_NAMES[out.path],

@@ -4,6 +4,7 @@ oracle cache, then copied bit for bit into the product's device cache."""
 from __future__ import annotations
 
 import json
+import os
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -129,25 +130,59 @@ def make_case(
     return Case(dtype, cache, query, tables, lengths, num_heads)
 
 
-def max_abs_err(actual: torch.Tensor, expected: np.ndarray) -> float:
-    a = actual.detach().float().cpu().numpy()
-    return float(np.max(np.abs(a - expected)))
+# Every parity check of the session, for the summary tests/conftest.py prints
+# at the end of the run: (test id, dtype, strict max-abs error, tolerance,
+# elements that took the output-rounding allowance, largest error among them).
+PARITY_LOG: list[tuple[str, str, float, float, int, float]] = []
+
+_DTYPE_NAMES = {torch.float16: "float16", torch.bfloat16: "bfloat16", torch.float32: "float32"}
+
+
+def _current_test() -> str:
+    return os.environ.get("PYTEST_CURRENT_TEST", "?").rsplit(" (", 1)[0]
+
+
+def record_parity(dtype: str, err: float, tol: float, allowed: int = 0, allowed_err: float = 0.0) -> None:
+    PARITY_LOG.append((_current_test(), dtype, float(err), float(tol), int(allowed), float(allowed_err)))
+
+
+def max_abs_err(actual, expected: np.ndarray, dtype: str | None = None) -> float:
+    """Strict max-abs error of a kernel output (a tensor, or its fp32 numpy
+    copy with the output's `dtype` name) against the oracle, recorded for
+    the end-of-run parity summary."""
+    if isinstance(actual, torch.Tensor):
+        dtype = dtype or _DTYPE_NAMES.get(actual.dtype, str(actual.dtype))
+        actual = actual.detach().float().cpu().numpy()
+    assert dtype is not None, "a numpy output needs its dtype name"
+    err = float(np.max(np.abs(actual - expected))) if actual.size else 0.0
+    record_parity(dtype, err, ATOL.get(dtype, float("nan")))
+    return err
 
 
 def assert_close_up_to_output_rounding(out: torch.Tensor, expected: np.ndarray, dtype: str) -> None:
-    """|out - expected| <= ATOL + half an ulp of the output dtype at |expected|.
+    """|out - expected| <= ATOL everywhere, except where half an ulp of the
+    output dtype at |expected| exceeds half of ATOL (bf16 |x| >= 2, fp16
+    |x| >= 4): there the bound is ATOL + that half ulp.
 
-    Outputs near single V values of magnitude >= 4 (short or peaked
-    attention) are where half a bf16 ulp (2^-6) already exceeds 1e-2: the
-    rounding of the output itself, which every bf16-output kernel (the
-    reference's `.to(q.dtype)` included) incurs."""
+    Half a bf16 ulp at |x| in [4, 8) is 2^-7 ~ 7.8e-3, most of the 1e-2
+    budget: the rounding of the output itself, which every bf16-output
+    kernel (the reference's `.to(q.dtype)` included) incurs, so elements of
+    that size get it on top. Everywhere else the stated max-abs is strict.
+    The strict max-abs over all elements is recorded for the summary."""
     got = out.detach().float().cpu().numpy()
     assert not np.isnan(got).any(), "NaN in the kernel output"
     bits = {"bfloat16": 8, "float16": 11, "float32": 24}[dtype]  # significand bits
     _, e = np.frexp(np.abs(expected).astype(np.float64))
     half_ulp = np.ldexp(1.0, e - bits - 1)
-    excess = np.abs(got - expected) - (ATOL[dtype] + half_ulp)
-    assert excess.max() <= 0, f"max excess {excess.max()} (max abs err {np.abs(got - expected).max()})"
+    allowance = np.where(half_ulp > ATOL[dtype] / 2, half_ulp, 0.0)
+    err = np.abs(got - expected)
+    excess = err - (ATOL[dtype] + allowance)
+    took = allowance > 0
+    record_parity(dtype, float(err.max()) if err.size else 0.0, ATOL[dtype], int(took.sum()),
+                  float(err[took].max()) if took.any() else 0.0)
+    strict = err[~took]
+    assert excess.max() <= 0, (f"max excess {excess.max()} (max abs err {err.max()}, "
+                               f"{strict.max() if strict.size else 0.0} where the bound is strict)")
 
 
 @dataclass

@@ -254,6 +254,7 @@ def test_launch_config_reports_the_resolved_launch(dtype, heads_per_kv, partitio
     a = _args(dtype=dtype, num_heads=8 * heads_per_kv, num_kv_heads=8, partition_size=partition,
               max_context_len=8192)
     out = _lib.LaunchConfig()
+    out.struct_size = ctypes.sizeof(out)
     assert lib.ikl_paged_attention_launch_config(ctypes.byref(a), ctypes.byref(out)) == 0
     cfg = ops.launch_config(a)
     path, tile, waves, split = expect
@@ -264,6 +265,34 @@ def test_launch_config_reports_the_resolved_launch(dtype, heads_per_kv, partitio
     if split == "fixed_partitions" and partition > 0:
         assert cfg["workgroups"] == (8192 // partition) * 8 * a.batch
     assert lib.ikl_paged_attention_launch_config(ctypes.byref(a), None) == _lib.IKL_EINVAL
+
+
+def test_launch_config_honours_the_callers_struct_size():
+    """ikl_launch_config carries its size: the library rejects a struct
+    shorter than the first version and never writes past the size a caller
+    declares (a caller built against an older, shorter header)."""
+    lib = _lib.load()
+    assert lib.ikl_abi_version() == _lib.IKL_ABI_VERSION
+    a = _args(partition_size=512, max_context_len=8192)
+    out = _lib.LaunchConfig()
+    out.struct_size = 0
+    assert lib.ikl_paged_attention_launch_config(ctypes.byref(a), ctypes.byref(out)) == _lib.IKL_EINVAL
+    assert "struct_size" in lib.ikl_last_error().decode()
+    min_bytes = _lib.LaunchConfig.group_size.offset
+    out.struct_size = min_bytes - 1
+    assert lib.ikl_paged_attention_launch_config(ctypes.byref(a), ctypes.byref(out)) == _lib.IKL_EINVAL
+    # the first version's size: filled up to workgroups, group_size untouched
+    out.struct_size = min_bytes
+    out.group_size = -7
+    assert lib.ikl_paged_attention_launch_config(ctypes.byref(a), ctypes.byref(out)) == 0
+    assert out.struct_size == min_bytes and out.workgroups > 0 and out.group_size == -7
+    out.struct_size = ctypes.sizeof(out)
+    assert lib.ikl_paged_attention_launch_config(ctypes.byref(a), ctypes.byref(out)) == 0
+    assert out.group_size == 4
+    header = Path(__file__).resolve().parents[1] / "include" / "ikl_paged.h"
+    text = header.read_text()
+    assert f"#define IKL_LAUNCH_CONFIG_MIN_BYTES {min_bytes}" in text
+    assert f"#define IKL_ABI_VERSION {_lib.IKL_ABI_VERSION}" in text
 
 
 def test_autotune_reporters_are_none_before_a_launch():
@@ -513,3 +542,26 @@ def test_noalloc_rejects_a_split_beyond_its_scratch_without_a_gpu():
     assert lib.ikl_paged_attention_workspace_size(ctypes.byref(a)) > (16 << 20)
     assert lib.ikl_paged_attention_noalloc(ctypes.byref(a), None) == _lib.IKL_EWORKSPACE
     assert "scratch" in _lib.last_error()
+
+
+@pytest.mark.parametrize(
+    ("dtype", "table_width", "heads_per_kv", "reference_answer"),
+    [  # tests/test_attention.py:22-42 verbatim (head_dim 64, query_group_size 8)
+        (torch.float16, 8, 4, "tensorcore_short_context"),
+        (torch.bfloat16, 16, 32, "tensorcore_short_context"),
+        (torch.float16, 17, 32, "scalar_grouped"),
+        (torch.float32, 8, 32, "scalar_grouped"),
+        (torch.float16, 8, 1, "mha_fallback"),
+    ],
+)
+def test_reference_truth_table_under_the_name_mapping(dtype, table_width, heads_per_kv, reference_answer):
+    """The reference's truth table read through REFERENCE_PATH_NAMES: every
+    row agrees except table_width 17, where the reference's tensor-core
+    kernel stops (W <= 16) and this library's matrix-core kernel does not."""
+    got = ops.paged_decode_grouped_path(dtype=dtype, head_dim=64, table_width=table_width,
+                                        heads_per_kv=heads_per_kv, query_group_size=8)
+    mapped = ops.REFERENCE_PATH_NAMES[got]
+    if table_width > 16 and dtype in (torch.float16, torch.bfloat16) and heads_per_kv > 1:
+        assert (reference_answer, mapped) == ("scalar_grouped", "tensorcore_short_context")
+    else:
+        assert mapped == reference_answer

@@ -523,3 +523,38 @@ def test_max_context_len_below_a_context_is_rejected():
     out = ops.paged_decode_attention_hip(*args, partition_size=512, max_context_len=1500)
     torch.cuda.synchronize()
     assert max_abs_err(out, case.expected()) <= ATOL["bfloat16"]
+
+
+@pytest.mark.parametrize("dtype,heads,kv", [("bfloat16", 32, 8), ("float16", 16, 16), ("float32", 8, 2),
+                                            ("bfloat16", 32, 1)])
+@pytest.mark.parametrize("partition_size", [None, -1, 64, -2])
+def test_nan_key_inside_the_context_propagates_like_the_reference(dtype, heads, kv, partition_size):
+    """A NaN in one attended key row makes every query head of that KV head
+    NaN for that request, as paged_reference's softmax does
+    (attention.py:18-36); other heads and requests stay finite and within
+    tolerance. Keys past a context (NaN poison, never attended) are covered
+    by the other tests."""
+    from inferkernellab_amd import ops
+
+    if partition_size == -2 and dtype == "float32":
+        pytest.skip("the balanced split runs on the MFMA family (fp16 / bf16)")
+    lengths = [300, 45, 700]
+    case = make_case(batch=3, num_heads=heads, num_kv_heads=kv, head_dim=64, block_size=16,
+                     lengths=lengths, dtype=dtype, seed=90 + heads)
+    oc = case.oracle_cache
+    bad_head = kv - 1
+    slot = oc.slot_mapping(case.tables[2], 123, 1)[0]  # request 2, position 123
+    nan = np.uint16(0x7FC0) if dtype == "bfloat16" else np.nan
+    oc.k[0, slot // 16, slot % 16, bad_head, 5] = nan
+    print(f"nan-key case dtype={dtype} H={heads} Hkv={kv} partition={partition_size}", flush=True)
+    out = ops.paged_decode_attention_hip(case.device_query(), case.device_cache(), case.device_tables(),
+                                         case.device_lengths(), partition_size=partition_size)
+    torch.cuda.synchronize()
+    expected = case.expected()
+    got = out.float().cpu().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(expected))
+    per_kv = heads // kv
+    assert np.isnan(expected[2, bad_head * per_kv:(bad_head + 1) * per_kv]).all()
+    finite = ~np.isnan(expected)
+    assert finite.sum() == expected.size - per_kv * 64
+    assert np.abs(got[finite] - expected[finite]).max() <= ATOL[dtype]

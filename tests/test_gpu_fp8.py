@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from oracle import paged_oracle as po
-from tests.helpers import ATOL, make_case, randn_storage, storage_to_torch
+from tests.helpers import ATOL, make_case, max_abs_err, randn_storage, storage_to_torch
 
 pytestmark = pytest.mark.gpu
 
@@ -115,7 +115,7 @@ def test_fp8_decode_attention_matches_oracle(act, heads, kv, dim, bs, lengths, p
     torch.cuda.synchronize()
     out = got.float().cpu().numpy()
     assert not np.isnan(out).any()
-    assert float(np.max(np.abs(out - _expected(base)))) < ATOL[act]
+    assert max_abs_err(out, _expected(base), act) < ATOL[act]
 
 
 def test_fp8_append_then_attention_and_quantisation_error():
@@ -157,7 +157,7 @@ def test_fp8_append_then_attention_and_quantisation_error():
     deq.v[0] = po.dequantize_rows_e4m3(vcodes, vs)
     exp = po.paged_decode_attention(q.float().numpy(), deq, tables, lengths)
     got = out.float().cpu().numpy()
-    assert float(np.max(np.abs(got - exp))) < ATOL["bfloat16"]
+    assert max_abs_err(got, exp, "bfloat16") < ATOL["bfloat16"]
     exact = po.paged_decode_attention(q.float().numpy(), ref16, tables, lengths)
     quant_err = float(np.max(np.abs(got - exact)))
     print(f"fp8 KV quantisation error vs bf16 rows: max abs {quant_err:.4f}")
@@ -203,4 +203,4 @@ def test_fp8_prefill_attention_matches_oracle(act, heads, kv, dim, bs, starts, e
     exp = po.paged_prefill_attention(po.to_f32(q, act), base.oracle_cache, base.tables, starts, ends)
     out = got.float().cpu().numpy()
     assert not np.isnan(out).any()
-    assert float(np.max(np.abs(out - exp))) < ATOL[act]
+    assert max_abs_err(out, exp, act) < ATOL[act]

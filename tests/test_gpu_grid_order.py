@@ -76,4 +76,4 @@ def test_request_fastest_grid_over_fp8_cache():
     torch.cuda.synchronize()
     out = got.float().cpu().numpy()
     assert not np.isnan(out).any()
-    assert float(np.max(np.abs(out - _expected(base)))) < ATOL["bfloat16"]
+    assert max_abs_err(out, _expected(base), "bfloat16") < ATOL["bfloat16"]

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from oracle import paged_oracle as po
-from tests.helpers import ATOL, make_case, make_prefill_case, storage_to_torch
+from tests.helpers import ATOL, make_case, make_prefill_case, max_abs_err, storage_to_torch
 
 pytestmark = pytest.mark.gpu
 
@@ -37,7 +37,7 @@ def test_decode_attention_on_head_major_cache(partition, heads, kv):
     out = ops.paged_decode_attention_hip_grouped(case.device_query(), cache, case.device_tables(),
                                                  case.device_lengths(), partition_size=partition)
     torch.cuda.synchronize()
-    assert float(np.max(np.abs(out.float().cpu().numpy() - case.expected()))) < ATOL["bfloat16"]
+    assert max_abs_err(out, case.expected()) < ATOL["bfloat16"]
 
 
 def test_folded_valu_workgroups_on_head_major_cache():
@@ -52,7 +52,7 @@ def test_folded_valu_workgroups_on_head_major_cache():
                                                  case.device_lengths())
     torch.cuda.synchronize()
     assert ops.paged_decode_grouped_autotune_config()["num_warps"] == 4
-    assert float(np.max(np.abs(out.float().cpu().numpy() - case.expected()))) < ATOL["float32"]
+    assert max_abs_err(out, case.expected()) < ATOL["float32"]
 
 
 def test_prefill_attention_on_head_major_cache():
@@ -65,7 +65,7 @@ def test_prefill_attention_on_head_major_cache():
                                 query_width=200)
     got = prep(case.device_query(), 0)
     torch.cuda.synchronize()
-    assert float(np.max(np.abs(got.float().cpu().numpy() - case.expected()))) < ATOL["bfloat16"]
+    assert max_abs_err(got, case.expected()) < ATOL["bfloat16"]
 
 
 def test_append_and_rope_append_into_head_major_cache():

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from tests.helpers import ATOL, make_prefill_case
+from tests.helpers import ATOL, make_prefill_case, max_abs_err
 
 pytestmark = pytest.mark.gpu
 
@@ -35,7 +35,7 @@ def _run(case, *, path=None, scale=None, query=None, out=None, layer=0, table_dt
 def _err(actual, expected):
     a = actual.detach().float().cpu().numpy()
     assert not np.isnan(a).any(), "NaN in the kernel output"
-    return float(np.max(np.abs(a - expected)))
+    return max_abs_err(actual, expected)
 
 
 def test_reference_case_fp32():
@@ -218,3 +218,41 @@ def test_table_entries_outside_the_cache_are_dropped(heads, kv, dim, bs, starts,
     torch.cuda.synchronize()
     assert prep.path == (path or "mfma_grouped")
     assert _err(got, _expected_dropping_blocks(case, dropped)) < ATOL[dtype]
+
+
+@pytest.mark.parametrize("dtype,path", [("bfloat16", None), ("float16", None), ("float32", None),
+                                        ("bfloat16", "scalar_grouped")])
+def test_nan_key_inside_the_context_propagates_like_the_reference(dtype, path):
+    """A NaN in one key row inside the prefix makes the query rows that
+    attend it NaN (rows at or past its position, for the query heads of its
+    KV head), and only those, as the reference's causal SDPA does
+    (attention.py:230-321: a NaN score under a boolean mask is kept for
+    allowed positions and masked out for the others). The MFMA prefill is
+    built without NaN semantics for its own arithmetic (it produces no NaN
+    of its own); a NaN from the cache still reaches the row sum and the PV
+    product, so the output row is NaN."""
+    heads, kv, dim, bs = 16, 4, 64, 16
+    starts, ends = [0, 40, 10], [77, 200, 90]
+    case = make_prefill_case(starts=starts, ends=ends, width=160, num_heads=heads, num_kv_heads=kv,
+                             head_dim=dim, block_size=bs, dtype=dtype, seed=33)
+    oc = case.base.oracle_cache
+    nan = np.uint16(0x7FC0) if dtype == "bfloat16" else np.nan
+    # request 1: a key inside its chunk (position 50) and request 2: one in
+    # the prefix before its chunk (position 4)
+    for b, pos, h in ((1, 50, 1), (2, 4, 3)):
+        slot = oc.slot_mapping(case.base.tables[b], pos, 1)[0]
+        oc.k[0, slot // bs, slot % bs, h, 7] = nan
+    print(f"prefill nan-key case dtype={dtype} path={path}", flush=True)
+    got, prep = _run(case, path=path)
+    out = got.float().cpu().numpy()
+    expected = case.expected()
+    nan_rows = np.isnan(expected)
+    assert np.array_equal(np.isnan(out), nan_rows)
+    per_kv = heads // kv
+    # request 1, heads of kv head 1: rows of positions >= 50 (t >= 10) are NaN, earlier rows finite
+    assert nan_rows[1, per_kv:2 * per_kv, 10:ends[1] - starts[1]].all()
+    assert not nan_rows[1, per_kv:2 * per_kv, :10].any()
+    # request 2, heads of kv head 3: every row of the chunk attends position 4
+    assert nan_rows[2, 3 * per_kv:4 * per_kv, :ends[2] - starts[2]].all()
+    finite = ~nan_rows
+    assert np.abs(out[finite] - expected[finite]).max() <= ATOL[dtype]
