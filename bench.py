@@ -917,25 +917,26 @@ def append_matches(w) -> bool:
     each request's slot: bit for bit for a 16-bit cache, the codes and
     scales quantize_rows_e4m3 gives for the FP8 cache."""
     cache, bs = w["cache"], w["block_size"]
-    slots = w["slots"].long()
+    # k / v are [layers, blocks, block_size, kv_heads, D] views whatever the
+    # storage order; the FP8 scales are [layers, blocks, kv_heads, block_size]
+    assert tuple(cache.k.shape[1:3]) == (w["pool"], bs)
+    slots = w["slots"].long().cpu()
     blk, off = slots // bs, slots % bs
+    assert int(blk.max()) < w["pool"] and int(off.max()) < bs
+    blk, off = blk.to(cache.k.device), off.to(cache.k.device)
     if w["fp8"]:
         from inferkernellab_amd.cache import quantize_rows_e4m3
 
+        assert tuple(cache.k_scale.shape[1:]) == (w["pool"], w["kv_heads"], bs)
         ok = True
         for new, codes, scales in ((w["new_k"], cache.k, cache.k_scale), (w["new_v"], cache.v, cache.v_scale)):
             c, sc = quantize_rows_e4m3(new)
-            if cache.head_major:
-                got_c = codes[0][blk, :, off]
-            else:
-                got_c = codes[0][blk, off]
-            ok = ok and torch.equal(got_c.view(torch.uint8), c.view(torch.uint8))
+            ok = ok and torch.equal(codes[0][blk, off].view(torch.uint8), c.view(torch.uint8))
             ok = ok and torch.equal(scales[0][blk, :, off], sc)
         return bool(ok)
     views = []
     for new, t in ((w["new_k"], cache.k), (w["new_v"], cache.v)):
-        got = t[0][blk, :, off] if cache.head_major else t[0][blk, off]
-        views.append(torch.equal(got.view(torch.int16), new.view(torch.int16)))
+        views.append(torch.equal(t[0][blk, off].view(torch.int16), new.view(torch.int16)))
     return all(views)
 
 

@@ -73,6 +73,18 @@ struct mfma_ops<f16_tag> {
 
 __device__ inline v4u32 zero4() { return v4u32{0u, 0u, 0u, 0u}; }
 
+// Orders the wave's LDS accesses on either side of it for every lane. Lanes
+// of one wave exchange tiles through LDS (one lane stores what another
+// loads); without a fence the compiler may treat LDS as memory private to
+// each thread and move or forward a load across another lane's store (it did
+// for a store guarded to half the lanes: the other half kept the previous
+// tile's value). Wavefront scope: no instruction beyond the ordering.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 typedef __attribute__((address_space(3))) s16x4_t *lds_s4_ptr;
 
 // ds_read_b64_tr_b16 of the 8-byte chunk this lane supplies (see above).

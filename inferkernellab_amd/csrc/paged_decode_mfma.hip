@@ -10,12 +10,14 @@
 //   online softmax on S (lane = one head x 4 tokens; lazily rescaled)
 //   O^T[D x 16 heads]     += V^T[D x 16] . P[16 x 16]   D/16 v_mfma_f32_16x16x16
 //
-// K rows feed the QK^T MFMA straight from HBM (lane l loads 16 bytes of
-// token l%16), and the S accumulator of lane l — P[tokens 4(l/16)..+3][head
-// l%16] — is already the B operand of the PV MFMA. V tiles are staged
-// row-major in LDS (16-byte pieces rotated by row to spread banks) and read
-// back transposed with ds_read_b64_tr_b16, which hands each lane four
-// consecutive tokens of one head_dim column: the V^T operand.
+// K and V tiles are loaded as whole rows (each load instruction covers
+// 64 / (D * elem / 16) complete rows) and staged row-major in LDS (16-byte
+// pieces rotated by row to spread banks). K comes back in the QK^T operand
+// layout (lane l: 16 bytes of token l%16); V comes back transposed with
+// ds_read_b64_tr_b16, which hands each lane four consecutive tokens of one
+// head_dim column: the V^T operand. The S accumulator of lane l —
+// P[tokens 4(l/16)..+3][head l%16] — is already the B operand of the PV
+// MFMA.
 //
 // Two schedules share that tile loop:
 //  * fixed partitions (paged_decode_mfma_kernel): a workgroup of WAVES
@@ -110,20 +112,26 @@ struct WaveTiles {
   static constexpr int CPIECES = D * CEB / 16;              // 16-byte pieces per cache row
   static constexpr int VLOADS = (TILE * CPIECES + 63) / 64; // 16-byte V loads per lane per tile
   static constexpr int VT_BYTES = TILE * ROWB;              // one staged V tile
+  static constexpr int KROWB = D * CEB;                     // bytes per staged K row (codes for KV8)
+  static constexpr int KT_BYTES = TILE * KROWB;             // one staged K tile
+  static constexpr int TILE_BYTES = VT_BYTES + KT_BYTES;    // a wave's LDS during the tile loop
+  // LDS reads of the QK^T operands per tile: one per k-step (16-bit; KV8
+  // with odd KSTEPS, 8 bytes each), or one 16-byte read per two k-steps
+  static constexpr int KREADS = KV8 && KSTEPS % 2 == 0 ? KSTEPS / 2 : KSTEPS;
   static constexpr int SROW = D + 4;                        // staged fp32 row (padded vs bank conflicts)
   static constexpr int ST_BYTES = NH * SROW * 4;            // one staged [NH heads x D] block
   using ops = mfma_ops<Tag>;
   typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 
   struct Tile {
-    v4u32 k[KSTEPS];       // 16-bit: one operand per k-step; KV8: raw codes, 8 bytes per k-step
+    v4u32 k[VLOADS];       // whole K rows, as V (KV8: codes)
     v4u32 v[VLOADS];
     f32x4_t ks, vs;        // KV8: scales of tokens 4 grp .. +3
     int n_valid;  // tokens of the tile inside the run with a valid block (0..16)
   };
 
   int lane, hl, grp;
-  int k_lane;
+  int k_lane[VLOADS], k_lds[VLOADS], k_rd[KREADS];
   int v_lds[VLOADS], v_lane[VLOADS], tr_lds[MTILES];
   v4u32 qb[NG][KSTEPS];
   f32x4_t acc[NG][MTILES];
@@ -136,16 +144,28 @@ struct WaveTiles {
     lane = threadIdx.x & 63;
     hl = lane & 15;   // MFMA row/column index inside a 16-lane group
     grp = lane >> 4;  // 16-lane group
-    k_lane = hl * (int)p.k_st * CEB + k_elem(0) * CEB;  // token hl, first element of k-step 0 (bytes)
 #pragma unroll
     for (int u = 0; u < VLOADS; ++u) {
-      // V cache piece: row pi / CPIECES, piece pi % CPIECES; for KV8 it widens
-      // into staged pieces 2c, 2c + 1
+      // K and V cache piece: row pi / CPIECES, piece pi % CPIECES, so each
+      // load instruction covers whole rows (a row is one contiguous
+      // D * CEB-byte run; loads that cover 16 rows x 64 bytes each, the
+      // MFMA operand's own shape, stream about 12 % slower on the GQA
+      // decode workload's tiles). For KV8 the V piece widens into staged
+      // pieces 2c, 2c + 1; K stays in codes.
       const int pi = u * 64 + lane;
       const int row = pi / CPIECES < TILE ? pi / CPIECES : TILE - 1, c = pi % CPIECES;
       const int sc = KV8 ? 2 * c : c;
       v_lds[u] = row * ROWB + ((sc + row) % PIECES) * 16;
       v_lane[u] = row * (int)p.v_st * CEB + c * 16;
+      k_lds[u] = row * KROWB + ((c + row) % CPIECES) * 16;
+      k_lane[u] = row * (int)p.k_st * CEB + c * 16;
+    }
+    // QK^T operand reads: k-step s of lane (hl, grp) is bytes [k_elem(s) CEB,
+    // +8 CEB) of staged row hl (16-byte pieces rotated by row, as stored)
+#pragma unroll
+    for (int r = 0; r < KREADS; ++r) {
+      const int byte = KV8 && KSTEPS % 2 == 0 ? k_elem(2 * r) : k_elem(r) * CEB;
+      k_rd[r] = hl * KROWB + (((byte >> 4) + hl) % CPIECES) * 16 + (byte & 15);
     }
 #pragma unroll
     for (int mt = 0; mt < MTILES; ++mt) {  // V^T reads: token 4g + (l%16)/4, dims 16mt + 4((l%16)%4)
@@ -171,9 +191,11 @@ struct WaveTiles {
 
   // Attends positions [t0, t1) of request b against kv head kvh (t0 is a
   // multiple of TILE) into fresh acc / m / lsum; lsum ends summed over the
-  // four lane groups. vtile: this wave's VT_BYTES of LDS.
+  // four lane groups. vtile: this wave's TILE_BYTES of LDS (the staged V
+  // tile, then the staged K tile).
   __device__ __forceinline__ void attend(const AttnParams &p, int64_t b, int kvh, int64_t t0, int64_t t1,
                                          char *vtile) {
+    char *const ktile = vtile + VT_BYTES;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
 #pragma unroll
@@ -216,21 +238,9 @@ struct WaveTiles {
           (void *)(kbase + (uint64_t)pu * kblk + off * kst), (short)0, (int)(nv * kst), 0x00020000);
       const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
           (void *)(vbase + (uint64_t)pu * vblk + off * vst), (short)0, (int)(nv * vst), 0x00020000);
+#pragma unroll
+      for (int u = 0; u < VLOADS; ++u) T.k[u] = __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane[u], 0, CPOL_NT);
       if constexpr (KV8) {
-        // KSTEPS contiguous 8-byte chunks at 8 KSTEPS grp: paired into
-        // 16-byte loads when KSTEPS is even, else 8-byte loads. T.k[s & ~1]
-        // holds k-step s (dwords xy for even s).
-        if constexpr (KSTEPS % 2 == 0) {
-#pragma unroll
-          for (int s = 0; s < KSTEPS; s += 2) T.k[s] = __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 8 * s, 0, CPOL_NT);
-        } else {
-#pragma unroll
-          for (int s = 0; s < KSTEPS; ++s) {
-            const u32x2v w = __builtin_amdgcn_raw_buffer_load_b64(kr, k_lane + 8 * s, 0, CPOL_NT);
-            if (s % 2 == 0) T.k[s] = v4u32{w.x, w.y, 0u, 0u};
-            else T.k[s - 1] = v4u32{T.k[s - 1].x, T.k[s - 1].y, w.x, w.y};
-          }
-        }
         // scales of tokens 4 grp .. +3 of the tile's block (16 bytes; a
         // masked block reads zero)
         const uint64_t so = (uint64_t)pu * (uint32_t)(p.s_sb * 4) + off * 4;
@@ -241,9 +251,6 @@ struct WaveTiles {
             __builtin_amdgcn_make_buffer_rsrc((void *)(vsbase + so), (short)0, sn, 0x00020000);
         T.ks = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ksr, 16 * grp, 0, CPOL_NT));
         T.vs = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vsr, 16 * grp, 0, CPOL_NT));
-      } else {
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) T.k[s] = __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * s, 0, CPOL_NT);
       }
 #pragma unroll
       for (int u = 0; u < VLOADS; ++u) T.v[u] = __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane[u], 0, CPOL_NT);
@@ -253,6 +260,7 @@ struct WaveTiles {
     // a masked block); full tiles skip the masking.
     auto compute = [&](Tile &T, auto mask) {
       constexpr bool MASK = decltype(mask)::value;
+      wave_lds_sync();  // the previous tile's LDS reads come before these stores
       // stage V row-major in LDS (rows past the tile are never read)
 #pragma unroll
       for (int u = 0; u < VLOADS; ++u) {
@@ -267,15 +275,31 @@ struct WaveTiles {
           }
         }
       }
+      // stage K rows (codes for KV8) the same way, then read the QK^T
+      // operands back in the MFMA layout: lane (hl, grp) takes row hl
+#pragma unroll
+      for (int u = 0; u < VLOADS; ++u) {
+        if (TILE * CPIECES % 64 == 0 || u * 64 + lane < TILE * CPIECES)
+          *reinterpret_cast<v4u32 *>(ktile + k_lds[u]) = T.k[u];
+      }
+      wave_lds_sync();  // every lane's stores come before any lane's reads
       // S^T of each group for tokens 4g' + i and head hl
       v4u32 ka[KSTEPS];
+      if constexpr (!KV8) {
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
-        if constexpr (KV8) {
-          const v4u32 w = T.k[s & ~1];
-          ka[s] = (s & 1) == 0 ? fp8x8_to<Tag>(w.x, w.y) : fp8x8_to<Tag>(w.z, w.w);
-        } else {
-          ka[s] = T.k[s];
+        for (int s = 0; s < KSTEPS; ++s) ka[s] = *reinterpret_cast<const v4u32 *>(ktile + k_rd[s]);
+      } else if constexpr (KSTEPS % 2 == 0) {
+#pragma unroll
+        for (int r = 0; r < KREADS; ++r) {
+          const v4u32 w = *reinterpret_cast<const v4u32 *>(ktile + k_rd[r]);
+          ka[2 * r] = fp8x8_to<Tag>(w.x, w.y);
+          ka[2 * r + 1] = fp8x8_to<Tag>(w.z, w.w);
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+          const u32x2v w = *reinterpret_cast<const u32x2v *>(ktile + k_rd[s]);
+          ka[s] = fp8x8_to<Tag>(w.x, w.y);
         }
       }
       f32x4_t sa[NG];
@@ -415,9 +439,10 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
   static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4, "1, 2 or 4 waves per workgroup");
   using WT = WaveTiles<Tag, D, NG, KV8>;
   constexpr int NH = WT::NH;
-  // LDS: each wave's V tile during the loop; at the end each wave's staged
-  // [NH heads x D] block, which the workgroup sums. The uses never overlap.
-  constexpr int SLOT = WT::ST_BYTES > WT::VT_BYTES ? WT::ST_BYTES : WT::VT_BYTES;
+  // LDS: each wave's V and K tiles during the loop; at the end each wave's
+  // staged [NH heads x D] block, which the workgroup sums. The uses never
+  // overlap.
+  constexpr int SLOT = WT::ST_BYTES > WT::TILE_BYTES ? WT::ST_BYTES : WT::TILE_BYTES;
   __shared__ __attribute__((aligned(16))) char lds[WAVES * SLOT];
   __shared__ float lds_m[WAVES][NH], lds_l[WAVES][NH];
 
@@ -451,7 +476,7 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
   const int nh = p.group_size < p.heads_per_kv - head0 ? p.group_size : p.heads_per_kv - head0;
   const int64_t hq0 = (int64_t)kvh * p.heads_per_kv + head0;
   wt.load_q(p, b, hq0, nh);
-  wt.attend(p, b, kvh, w_start, w_end, lds + wave * WT::VT_BYTES);
+  wt.attend(p, b, kvh, w_start, w_end, lds + wave * WT::TILE_BYTES);
 
   // combine the workgroup's waves: common max M per head, rescaled sums
   float M[NG], L[NG], f[NG];
@@ -491,7 +516,7 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
   float *const stage = reinterpret_cast<float *>(lds);
   wt.stage(stage + wave * NH * WT::SROW, f, nh);
   if constexpr (WAVES > 1) __syncthreads();
-  else __builtin_amdgcn_wave_barrier();
+  else wave_lds_sync();
   if (p.split) {
     const int64_t prow = (b * p.num_parts + part) * p.num_heads + hq0;
     store_rows_f32<D, NH, WAVES>(p.part_o + prow * D, stage, nh, threadIdx.x, 64 * WAVES);
@@ -601,9 +626,10 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
   static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4, "1, 2 or 4 waves per workgroup");
   using WT = WaveTiles<Tag, D, NG, KV8>;
   constexpr int NH = WT::NH;
-  // LDS: each wave's V tile during a piece; at its end each wave's staged
-  // [NH heads x D] block, which the workgroup sums (separated by barriers).
-  constexpr int SLOT = WT::ST_BYTES > WT::VT_BYTES ? WT::ST_BYTES : WT::VT_BYTES;
+  // LDS: each wave's V and K tiles during a piece; at its end each wave's
+  // staged [NH heads x D] block, which the workgroup sums (separated by
+  // barriers).
+  constexpr int SLOT = WT::ST_BYTES > WT::TILE_BYTES ? WT::ST_BYTES : WT::TILE_BYTES;
   __shared__ __attribute__((aligned(16))) char lds[WAVES * SLOT];
   __shared__ float lds_m[WAVES][NH], lds_l[WAVES][NH];
   const int lane = (int)(threadIdx.x & 63u);
@@ -637,7 +663,7 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
     const int64_t a0 = t_in + wave * n / WAVES, a1 = t_in + (wave + 1) * n / WAVES;
     const int64_t e = a1 * TILE < ctx ? a1 * TILE : ctx;
     wt.load_q(p, b, hq0, nh);
-    wt.attend(p, b, kvh, a0 * TILE, a1 > a0 ? e : a0 * TILE, lds + wave * WT::VT_BYTES);
+    wt.attend(p, b, kvh, a0 * TILE, a1 > a0 ? e : a0 * TILE, lds + wave * WT::TILE_BYTES);
 
     // combine the waves: common max M per head, rescaled sums
     float M[NG], L[NG], f[NG];
@@ -666,14 +692,14 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
         for (int k = 0; k < WAVES; ++k) L[gi] += lds_l[k][h] * fast_exp2(lds_m[k][h] - M[gi]);
       }
     } else {
-      __builtin_amdgcn_wave_barrier();
+      wave_lds_sync();
     }
 #pragma unroll
     for (int gi = 0; gi < NG; ++gi)
       f[gi] = (WAVES > 1 ? fast_exp2(wt.m[gi] - M[gi]) : 1.f) * (L[gi] > 0.f ? 1.f / L[gi] : 0.f);
     wt.stage(stage + wave * NH * WT::SROW, f, nh);
     if constexpr (WAVES > 1) __syncthreads();
-    else __builtin_amdgcn_wave_barrier();
+    else wave_lds_sync();
     const int64_t slot = b * U + u + w;
     store_rows_f32<D, NH, WAVES>(p.part_o + slot * p.group_size * D, stage, nh, (int)threadIdx.x, 64 * WAVES);
     if (wave == 0 && wt.grp == 0) {
@@ -684,7 +710,7 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
     }
     // the staged blocks are read before the next piece's V tiles overwrite them
     if constexpr (WAVES > 1) __syncthreads();
-    else __builtin_amdgcn_wave_barrier();
+    else wave_lds_sync();
 
     g += t_hi - t_in;
     if (g >= g1) break;
