@@ -77,6 +77,13 @@ struct AttnParams {
   // the slots are distinct and each unit's pieces are consecutive).
   int32_t sk_waves;
   int32_t units;           // kv heads x query groups per request
+  // Units per workgroup of the unit-parallel balanced split (1 = one-unit
+  // runs, as above). With sk_unitw = UW > 1 the sequence is request-major,
+  // then unit group (UW consecutive units), then position: the run's
+  // workgroup has UW waves, wave i attends unit ug * UW + i, and the piece
+  // of (request b, group ug) that run w covers lands in slots ((b * units /
+  // UW + ug) + w) * UW + i.
+  int32_t sk_unitw;
   int32_t grid_spread;     // fixed-partition MFMA grid is request-fastest (spread_grid)
   int64_t batch;
   int64_t cap_tokens;      // table_width * block_size: positions a table can map
@@ -216,10 +223,16 @@ hipError_t launch_mfma_attention(int dtype, int head_dim, const AttnParams &p, d
 struct MfmaShape {
   int tile_tokens, waves_per_workgroup, stages;
 };
-MfmaShape mfma_launch_shape(bool balanced, int group_size);
+MfmaShape mfma_launch_shape(bool balanced, int group_size, int unitw = 1);
 
 // Workgroups of the balanced-split MFMA kernel (for units of `group_size`
-// heads) resident at once on the current device.
-int mfma_streamk_capacity(int dtype, int head_dim, int group_size, bool kv_fp8);
+// heads; `unitw` units per workgroup for the unit-parallel form) resident at
+// once on the current device.
+int mfma_streamk_capacity(int dtype, int head_dim, int group_size, bool kv_fp8, int unitw = 1);
+
+// Units per workgroup the balanced split uses for `units` units of
+// `group_size` heads per request: the largest of 8, 4, 2 dividing `units`
+// for units of up to 16 heads, else 1 (one-unit runs).
+int mfma_streamk_unitw(int64_t units, int group_size);
 
 }  // namespace ikl

@@ -441,22 +441,25 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(const AttnParam
   int np;
   int64_t prow, pstride;
   if (p.sk_waves > 0) {
-    // balanced split: unit u's pieces sit in consecutive slots s + w for the
-    // runs w that cover its tiles; rows slot * group_size + head.
+    // balanced split: the pieces of unit u (group ug = u / UW, member i) sit
+    // in consecutive slots (b NUG + ug + w) UW + i for the runs w that cover
+    // its group's tiles (UW = 1: one-unit runs); rows slot * group_size + head.
     int64_t before;
     int own;
     const int64_t total = request_tiles(p, b, lane, &before, &own);
-    const int64_t U = p.units;
-    const int64_t T = U * total;
+    const int64_t UW = p.sk_unitw;
+    const int64_t NUG = p.units / UW;
+    const int64_t T = NUG * total;
     const int64_t W = (int64_t)p.sk_waves < T ? (int64_t)p.sk_waves : T;
     const int kvh = (int)(hq / p.heads_per_kv), r = (int)(hq % p.heads_per_kv);
     const int64_t u = (int64_t)kvh * p.groups_per_kv + r / p.group_size;
-    const int64_t s = U * before + u * own;  // first global tile of the unit
+    const int64_t ug = u / UW, ui = u - ug * UW;
+    const int64_t s = NUG * before + ug * own;  // first sequence entry of the group
     const int64_t w_lo = own > 0 ? wave_of_tile(s, T, W) : 0;
     const int64_t w_hi = own > 0 ? wave_of_tile(s + own - 1, T, W) : -1;
     np = (int)(w_hi - w_lo + 1);
-    prow = (b * U + u + w_lo) * p.group_size + r % p.group_size;
-    pstride = p.group_size;
+    prow = ((b * NUG + ug + w_lo) * UW + ui) * p.group_size + r % p.group_size;
+    pstride = UW * p.group_size;
   } else {
     const int64_t ctx = p.lens_i64 ? load_index<int64_t>(p.lens, b) : load_index<int32_t>(p.lens, b);
     np = ctx > 0 ? (int)((ctx + p.partition_size - 1) / p.partition_size) : 0;
@@ -541,6 +544,7 @@ struct Plan {
   int num_parts = 1;
   bool split = false;
   int sk_waves = 0;  // balanced split (MFMA family): runs (workgroups) sharing the batch's tiles
+  int sk_unitw = 1;  // units per balanced-split workgroup (unit-parallel form when > 1)
   int64_t units = 0;  // kv heads x query groups per request
   int64_t ws_o_bytes = 0;
   int64_t ws_bytes = 0;
@@ -701,15 +705,23 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl, bool fold_waves = tru
       a->partition_size == -2 ||
       (a->partition_size == 0 && pl.path == IKL_PATH_MFMA_GROUPED && (t_max > SK_MIN_BATCH_TILES || past_one_round));
   if (want_balanced && cap < (int64_t(1) << 29)) {
-    const int64_t skw = mfma_launch_shape(true, pl.group_size).waves_per_workgroup;
-    const int64_t w = std::min<int64_t>(mfma_streamk_capacity(a->dtype, a->head_dim, pl.group_size, pl.kv_fp8),
-                                        std::max<int64_t>((t_max + SK_MIN_TILES * skw - 1) / (SK_MIN_TILES * skw), 1));
-    if ((double)(t_max + 1) * (double)w < 4.0e18) {
+    // Units of up to 16 heads run unit-parallel (workgroups of UW waves, one
+    // unit each, walking the same request tiles): the GQA decode workload's
+    // kernel (32/8 hd128 bf16 B32 x U[4096, 8192]) streams faster that way
+    // than as one-unit runs. Sequence entries: units / UW per request tile.
+    const int uw = mfma_streamk_unitw(pl.units, pl.group_size);
+    const int64_t t_seq = t_max / uw;
+    const int64_t skw = uw > 1 ? 1 : mfma_launch_shape(true, pl.group_size).waves_per_workgroup;
+    const int64_t w =
+        std::min<int64_t>(mfma_streamk_capacity(a->dtype, a->head_dim, pl.group_size, pl.kv_fp8, uw),
+                          std::max<int64_t>((t_seq + SK_MIN_TILES * skw - 1) / (SK_MIN_TILES * skw), 1));
+    if ((double)(t_seq + 1) * (double)w < 4.0e18) {
       pl.sk_waves = (int)w;
+      pl.sk_unitw = uw;
       pl.split = true;
       pl.num_parts = 1;
-      pl.partition = (int)std::min<int64_t>(16 * ((t_max + w - 1) / w), 0x7fffffffLL);
-      const int64_t rows = (units + w) * pl.group_size;
+      pl.partition = (int)std::min<int64_t>(16 * ((t_seq + w - 1) / w), 0x7fffffffLL);
+      const int64_t rows = (units / uw + w) * uw * pl.group_size;
       pl.ws_o_bytes = ((rows * a->head_dim * 4) + 255) / 256 * 256;
       pl.ws_bytes = pl.ws_o_bytes + rows * 4;
       return IKL_OK;
@@ -895,7 +907,7 @@ extern "C" int ikl_paged_attention_launch_config(const ikl_paged_attention_args 
   c.path = pl.path;
   c.partition_size = pl.split ? pl.partition : 0;
   if (pl.path == IKL_PATH_MFMA_GROUPED) {
-    const MfmaShape sh = mfma_launch_shape(pl.sk_waves > 0, pl.group_size);
+    const MfmaShape sh = mfma_launch_shape(pl.sk_waves > 0, pl.group_size, pl.sk_unitw);
     c.tile_tokens = sh.tile_tokens;
     c.waves_per_workgroup = sh.waves_per_workgroup;
     c.stages = sh.stages;
@@ -999,6 +1011,7 @@ int run_attention(const ikl_paged_attention_args *a, const Plan &pl, const Fused
   p.lens_i64 = a->lens_type == IKL_I64;
   p.scale_log2 = a->scale * LOG2E;
   p.sk_waves = pl.sk_waves;
+  p.sk_unitw = pl.sk_unitw;
   p.units = (int32_t)pl.units;
   p.grid_spread = pl.path == IKL_PATH_MFMA_GROUPED && pl.sk_waves == 0 && spread_grid(pl.units, pl.num_parts, a->batch);
   p.batch = a->batch;

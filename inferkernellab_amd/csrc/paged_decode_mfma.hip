@@ -193,8 +193,18 @@ struct WaveTiles {
   // multiple of TILE) into fresh acc / m / lsum; lsum ends summed over the
   // four lane groups. vtile: this wave's TILE_BYTES of LDS (the staged V
   // tile, then the staged K tile).
+  //
+  // LOCKSTEP: the wave meets a workgroup barrier (no memory fence) every
+  // two tiles, so the waves of a workgroup that walk the same blocks stay
+  // together (every wave must call with the same tile count). has_pre_win:
+  // pre_win is the table window starting at t0's block, already loaded by
+  // the caller.
+  // q_nh > 0: load the Q^T operands of heads [q_hq0, q_hq0 + q_nh) here,
+  // after the first tile's loads are issued, so their latency overlaps.
+  template <bool LOCKSTEP = false>
   __device__ __forceinline__ void attend(const AttnParams &p, int64_t b, int kvh, int64_t t0, int64_t t1,
-                                         char *vtile) {
+                                         char *vtile, bool has_pre_win = false, int pre_win = 0,
+                                         int64_t q_hq0 = 0, int q_nh = 0) {
     char *const ktile = vtile + VT_BYTES;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
@@ -215,7 +225,7 @@ struct WaveTiles {
     const uint32_t kst = (uint32_t)(p.k_st * CEB), vst = (uint32_t)(p.v_st * CEB);
     const int bs = p.block_size;
     int64_t win_base = p.bs_shift >= 0 ? (t0 >> p.bs_shift) : t0 / bs;
-    int win = load_table_window(p, b, win_base, lane);
+    int win = has_pre_win ? pre_win : load_table_window(p, b, win_base, lane);
 
     // Resolves tile t's block and issues its K/V loads through buffer
     // resources whose record count ends at the tile's last valid row: rows
@@ -375,10 +385,15 @@ struct WaveTiles {
       if (T.n_valid == TILE) compute(T, std::false_type{});
       else compute(T, std::true_type{});
     };
-    // software pipeline: the next tile's loads fly while a tile computes
+    // software pipeline: the next tile's loads fly while a tile computes (a
+    // tile's registers taking the load two ahead right after it is staged
+    // in LDS measured slower: GQA 32/8 hd128 bf16 B32 x U[4096, 8192]
+    // 124.5 -> 126-128 us, its FP8-cache form 73 -> 80 us)
     Tile ta, tb;
     issue(0, ta);
+    if (q_nh > 0) load_q(p, b, q_hq0, q_nh);
     for (int t = 0; t < n_tiles; t += 2) {
+      if constexpr (LOCKSTEP) __builtin_amdgcn_s_barrier();
       issue(t + 1, tb);
       run(ta);
       issue(t + 2, ta);
@@ -554,7 +569,7 @@ __device__ __forceinline__ int64_t uniform64(int64_t x) {
 
 __device__ __forceinline__ SkRun sk_run(const AttnParams &p, int64_t w, int lane) {
   SkRun r{0, 0, -1, 0, 0, false};
-  const int64_t U = p.units;
+  const int64_t U = p.units / p.sk_unitw;  // sequence entries per request tile
   // total tiles, then the request holding the run's first tile (a batch
   // of up to 64 requests takes one scan for both)
   int64_t total;
@@ -611,6 +626,17 @@ __device__ __forceinline__ void sk_next_request(const AttnParams &p, int64_t &b,
     pb += nb;
     ++b;
     nb = __builtin_amdgcn_readfirstlane((int)((clamped_ctx(p, b) + 15) >> 4));
+  } while (nb == 0);
+}
+
+// sk_next_request, also handing back the new request's clamped length.
+__device__ __forceinline__ void sk_next_request_ctx(const AttnParams &p, int64_t &b, int &nb, int64_t &pb,
+                                                    int64_t &ctx) {
+  do {
+    pb += nb;
+    ++b;
+    ctx = uniform64(clamped_ctx(p, b));
+    nb = (int)((ctx + 15) >> 4);
   } while (nb == 0);
 }
 
@@ -718,6 +744,91 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
   }
 }
 
+// Unit-parallel balanced split: p.sk_waves workgroups of UW waves, for
+// units of up to 16 heads. The sequence is request-major, then unit group
+// (UW consecutive units), then tile; workgroup w takes the run [w T / W,
+// (w + 1) T / W) of it and its wave i attends unit ug * UW + i over each
+// piece — so the UW waves read their heads' rows of the same cache blocks
+// at about the same time (in the token-major cache those rows interleave
+// inside each block). A load-only probe of the GQA 32/8 hd128 bf16 B32 x
+// U[4096, 8192] pattern streams it in 115 us this way against 126 us as
+// one-unit runs. The waves meet a barrier every two tiles, which keeps them
+// on the same blocks (C4 shape kernel 131 -> 127 us; every wave of the
+// workgroup walks the same tile counts); they share no LDS. Each writes its
+// own unit's normalised partial and log2-sum-exp per piece, to slot
+// ((b * NUG + ug) + w) * UW + i (NUG = units / UW groups per request).
+// While a piece runs, the next piece's context length and first table
+// window are already loaded, and each piece's Q rows load behind its first
+// tile's K/V, so a piece boundary exposes one memory round trip instead of
+// three.
+template <typename Tag, int D, int UW, bool KV8>
+__global__ __launch_bounds__(64 * UW) __attribute__((amdgpu_waves_per_eu(2, 8))) void paged_decode_mfma_unitk_kernel(
+    const AttnParams p) {
+  using WT = WaveTiles<Tag, D, 1, KV8>;
+  constexpr int NH = WT::NH;
+  // LDS: per wave, its V and K tiles during a piece, then its staged
+  // [NH heads x D] block (the wave's own region; waves do not share LDS)
+  constexpr int SLOT = WT::ST_BYTES > WT::TILE_BYTES ? WT::ST_BYTES : WT::TILE_BYTES;
+  __shared__ __attribute__((aligned(16))) char lds[UW * SLOT];
+  const int lane = (int)(threadIdx.x & 63u);
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t NUG = p.units / UW;
+  const int64_t w = blockIdx.x;
+  const SkRun run = sk_run(p, w, lane);
+  if (!run.active) return;
+  const int64_t g1 = run.g1;
+  int64_t g = run.g0, b = run.b, pb = run.pb;
+  int nb = run.nb;
+  char *const mine = lds + wave * SLOT;
+  float *const stage = reinterpret_cast<float *>(mine);
+
+  WT wt(p);
+  int64_t ctx = uniform64(clamped_ctx(p, b));
+  int win = 0;
+  bool have_win = false;
+  while (true) {
+    // piece: unit group ug of request b, request tiles [t_in, t_hi)
+    const int64_t rel = g - NUG * pb;
+    const int64_t ug = rel / nb;
+    const int64_t t_in = rel - ug * nb;
+    const int64_t t_hi = (int64_t)nb < t_in + (g1 - g) ? (int64_t)nb : t_in + (g1 - g);
+    const int u = (int)ug * UW + wave;
+    const int kvh = u / p.groups_per_kv, qg = u % p.groups_per_kv;
+    const int head0 = qg * p.group_size;
+    const int nh = p.group_size < p.heads_per_kv - head0 ? p.group_size : p.heads_per_kv - head0;
+    const int64_t hq0 = (int64_t)kvh * p.heads_per_kv + head0;
+    const int64_t e = t_hi * TILE < ctx ? t_hi * TILE : ctx;
+    // the run's next piece starts at tile 0 of group ug + 1, or of the next
+    // request with tiles: its length and first window load now
+    const int64_t gn = g + (t_hi - t_in);
+    int64_t bn = b, pbn = pb, ctxn = ctx;
+    int nbn = nb, win_n = 0;
+    if (gn < g1) {
+      if (t_hi == nb && ug == NUG - 1) sk_next_request_ctx(p, bn, nbn, pbn, ctxn);  // one exists: gn < T
+      win_n = load_table_window(p, bn, 0, lane);
+    }
+    wt.template attend<true>(p, b, kvh, t_in * TILE, e, mine, have_win, win, hq0, nh);
+    const float L = wt.lsum[0], M = wt.m[0];
+    const float f[1] = {L > 0.f ? 1.f / L : 0.f};
+    wave_lds_sync();  // the tile loop's LDS reads come before the staged block
+    wt.stage(stage, f, nh);
+    wave_lds_sync();
+    const int64_t slot = ((b * NUG + ug) + w) * UW + wave;
+    store_rows_f32<D, NH, 1>(p.part_o + slot * p.group_size * D, stage, nh, lane, 64);
+    if (wt.grp == 0 && wt.hl < nh) p.part_lse[slot * p.group_size + wt.hl] = L > 0.f ? M + log2f(L) : -INFINITY;
+    wave_lds_sync();  // the staged block is read before the next piece's tiles overwrite it
+
+    g = gn;
+    if (g >= g1) break;
+    b = bn;
+    pb = pbn;
+    nb = nbn;
+    ctx = ctxn;
+    win = win_n;
+    have_win = true;
+  }
+}
+
 // Waves sharing one fixed partition: 4 for 16-head units; 2 for 32-head
 // units (their staged [32 x D] blocks would exceed 64 KB of LDS at 4).
 template <int NG>
@@ -739,6 +850,17 @@ constexpr int sk_wg_waves() {
 
 template <typename Tag, int D, int NG, bool KV8>
 void launch_shape(const AttnParams &p, dim3 grid, hipStream_t s) {
+  if constexpr (NG == 1) {
+    if (p.sk_waves > 0 && p.sk_unitw > 1) {
+      const dim3 g((unsigned)p.sk_waves);
+      switch (p.sk_unitw) {
+        case 2: paged_decode_mfma_unitk_kernel<Tag, D, 2, KV8><<<g, dim3(128), 0, s>>>(p); break;
+        case 4: paged_decode_mfma_unitk_kernel<Tag, D, 4, KV8><<<g, dim3(256), 0, s>>>(p); break;
+        default: paged_decode_mfma_unitk_kernel<Tag, D, 8, KV8><<<g, dim3(512), 0, s>>>(p); break;
+      }
+      return;
+    }
+  }
   if (p.sk_waves > 0) {
     constexpr int SKW = sk_wg_waves<NG>();
     paged_decode_mfma_streamk_kernel<Tag, D, NG, SKW, KV8><<<dim3((unsigned)p.sk_waves), dim3(64 * SKW), 0, s>>>(p);
@@ -770,46 +892,59 @@ void launch_kv(int d, const AttnParams &p, dim3 grid, hipStream_t s) {
 // (CUs x workgroups per CU), cached per device; 256 CUs x the kernel's
 // waves per CU (8 for 16-head units, 4 for 32-head) / its waves per
 // workgroup when no device answers (planning on a host without a GPU).
-template <typename Tag, int D, int NG, bool KV8>
-int streamk_capacity_for() {
+template <typename K>
+int resident_capacity(K kernel, int threads, int waves_per_cu, std::atomic<int> *cache) {
   constexpr int MAX_DEV = 64;
-  constexpr int SKW = sk_wg_waves<NG>();
-  constexpr int FALLBACK = 256 * (NG == 1 ? 8 : 4) / SKW;
-  // Written once per device by whichever thread gets there first; every
-  // writer stores the same value, and readers see 0 (query again) or it.
-  static std::atomic<int> cache[MAX_DEV] = {};
+  const int fallback = 256 * waves_per_cu / (threads / 64);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) {
     (void)hipGetLastError();
-    return FALLBACK;
+    return fallback;
   }
+  // Written once per device by whichever thread gets there first; every
+  // writer stores the same value, and readers see 0 (query again) or it.
   const int known = cache[dev].load(std::memory_order_acquire);
   if (known > 0) return known;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_mfma_streamk_kernel<Tag, D, NG, SKW, KV8>,
-                                                   64 * SKW, 0) != hipSuccess ||
-      cus <= 0 || per_cu <= 0) {
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess || cus <= 0 ||
+      per_cu <= 0) {
     (void)hipGetLastError();
-    return FALLBACK;
+    return fallback;
   }
   cache[dev].store(cus * per_cu, std::memory_order_release);
   return cus * per_cu;
 }
 
+template <typename Tag, int D, int NG, bool KV8>
+int streamk_capacity_for(int unitw) {
+  constexpr int SKW = sk_wg_waves<NG>();
+  if constexpr (NG == 1) {
+    static std::atomic<int> c2[64] = {}, c4[64] = {}, c8[64] = {};
+    switch (unitw) {
+      case 2: return resident_capacity(paged_decode_mfma_unitk_kernel<Tag, D, 2, KV8>, 128, 8, c2);
+      case 4: return resident_capacity(paged_decode_mfma_unitk_kernel<Tag, D, 4, KV8>, 256, 8, c4);
+      case 8: return resident_capacity(paged_decode_mfma_unitk_kernel<Tag, D, 8, KV8>, 512, 8, c8);
+      default: break;
+    }
+  }
+  static std::atomic<int> c1[64] = {};
+  return resident_capacity(paged_decode_mfma_streamk_kernel<Tag, D, NG, SKW, KV8>, 64 * SKW, NG == 1 ? 8 : 4, c1);
+}
+
 template <typename Tag, int NG, bool KV8>
-int capacity_dim(int d) {
+int capacity_dim(int d, int unitw) {
   switch (d) {
-    case 32: return streamk_capacity_for<Tag, 32, NG, KV8>();
-    case 64: return streamk_capacity_for<Tag, 64, NG, KV8>();
-    case 96: return streamk_capacity_for<Tag, 96, NG, KV8>();
-    default: return streamk_capacity_for<Tag, 128, NG, KV8>();
+    case 32: return streamk_capacity_for<Tag, 32, NG, KV8>(unitw);
+    case 64: return streamk_capacity_for<Tag, 64, NG, KV8>(unitw);
+    case 96: return streamk_capacity_for<Tag, 96, NG, KV8>(unitw);
+    default: return streamk_capacity_for<Tag, 128, NG, KV8>(unitw);
   }
 }
 
 template <typename Tag, int NG>
-int capacity_kv(int d, bool kv8) {
-  return kv8 ? capacity_dim<Tag, NG, true>(d) : capacity_dim<Tag, NG, false>(d);
+int capacity_kv(int d, bool kv8, int unitw) {
+  return kv8 ? capacity_dim<Tag, NG, true>(d, unitw) : capacity_dim<Tag, NG, false>(d, unitw);
 }
 
 }  // namespace
@@ -832,16 +967,25 @@ hipError_t launch_mfma_attention(int dtype, int head_dim, const AttnParams &p, d
   return hipGetLastError();
 }
 
-MfmaShape mfma_launch_shape(bool balanced, int group_size) {
+MfmaShape mfma_launch_shape(bool balanced, int group_size, int unitw) {
+  if (balanced && group_size <= 16 && unitw > 1) return MfmaShape{TILE, unitw, 2};
   const int waves = group_size > 16 ? (balanced ? sk_wg_waves<2>() : wg_waves<2>())
                                     : (balanced ? sk_wg_waves<1>() : wg_waves<1>());
   return MfmaShape{TILE, waves, 2};
 }
 
-int mfma_streamk_capacity(int dtype, int head_dim, int group_size, bool kv_fp8) {
+int mfma_streamk_capacity(int dtype, int head_dim, int group_size, bool kv_fp8, int unitw) {
   const bool bf = dtype == IKL_BF16, two = group_size > 16;
-  if (bf) return two ? capacity_kv<bf16_tag, 2>(head_dim, kv_fp8) : capacity_kv<bf16_tag, 1>(head_dim, kv_fp8);
-  return two ? capacity_kv<f16_tag, 2>(head_dim, kv_fp8) : capacity_kv<f16_tag, 1>(head_dim, kv_fp8);
+  if (bf)
+    return two ? capacity_kv<bf16_tag, 2>(head_dim, kv_fp8, 1) : capacity_kv<bf16_tag, 1>(head_dim, kv_fp8, unitw);
+  return two ? capacity_kv<f16_tag, 2>(head_dim, kv_fp8, 1) : capacity_kv<f16_tag, 1>(head_dim, kv_fp8, unitw);
+}
+
+int mfma_streamk_unitw(int64_t units, int group_size) {
+  if (group_size > 16) return 1;
+  for (int c : {8, 4, 2})
+    if (units % c == 0) return c;
+  return 1;
 }
 
 }  // namespace ikl

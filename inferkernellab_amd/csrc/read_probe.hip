@@ -17,19 +17,26 @@ constexpr int PROBE_THREADS = 256;
 constexpr int PROBE_UNROLL = 4;  // 16-byte loads in flight per thread
 constexpr uint32_t PROBE_TAG = 0x9e3779b9u;
 
+// Workgroup w streams its own contiguous chunk [w n16 / G, (w + 1) n16 / G)
+// of 16-byte pieces front to back (PROBE_UNROLL loads in flight per
+// thread). Chunks per workgroup stream markedly faster than a grid-stride
+// sweep of the same buffer (6.6-6.7 against 5.1-5.9 TB/s measured on
+// MI355X for 512 MiB - 1 GiB), which interleaves every wave's loads over
+// the whole buffer.
 __global__ __launch_bounds__(PROBE_THREADS) void hbm_read_probe_kernel(const v4u32 *__restrict__ src, int64_t n16,
                                                                         uint32_t *sink) {
-  const int64_t stride = (int64_t)gridDim.x * PROBE_THREADS;
-  int64_t i = (int64_t)blockIdx.x * PROBE_THREADS + threadIdx.x;
+  const int64_t lo = (int64_t)blockIdx.x * n16 / gridDim.x, hi = ((int64_t)blockIdx.x + 1) * n16 / gridDim.x;
+  constexpr int STEP = PROBE_THREADS * PROBE_UNROLL;
   uint32_t acc = 0;
-  for (; i + (PROBE_UNROLL - 1) * stride < n16; i += PROBE_UNROLL * stride) {
+  int64_t i = lo + threadIdx.x;
+  for (; i + (PROBE_UNROLL - 1) * PROBE_THREADS < hi; i += STEP) {
     v4u32 v[PROBE_UNROLL];
 #pragma unroll
-    for (int u = 0; u < PROBE_UNROLL; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
+    for (int u = 0; u < PROBE_UNROLL; ++u) v[u] = __builtin_nontemporal_load(src + i + u * PROBE_THREADS);
 #pragma unroll
     for (int u = 0; u < PROBE_UNROLL; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
   }
-  for (; i < n16; i += stride) {
+  for (; i < hi; i += PROBE_THREADS) {
     const v4u32 v = __builtin_nontemporal_load(src + i);
     acc ^= v.x ^ v.y ^ v.z ^ v.w;
   }

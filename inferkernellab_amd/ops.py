@@ -643,7 +643,12 @@ class PreparedPagedAttention:
     def kernel_names(self) -> tuple[str, str | None]:
         """(attention kernel, reduce kernel or None) this launch enqueues."""
         if self.path == "mfma_grouped":
-            main = "paged_decode_mfma_streamk_kernel" if self.balanced_split else "paged_decode_mfma_kernel"
+            if not self.balanced_split:
+                main = "paged_decode_mfma_kernel"
+            elif self.launch["group_size"] <= 16 and self.launch["num_warps"] > 1:
+                main = "paged_decode_mfma_unitk_kernel"  # unit-parallel: one unit per wave
+            else:
+                main = "paged_decode_mfma_streamk_kernel"
         else:
             main = "paged_decode_scalar_kernel"
         return main, ("paged_decode_reduce_kernel" if self.launch["split"] != "none" else None)

@@ -92,23 +92,25 @@ def test_partition_planning_for_the_gqa_decode_shape():
 
 
 def test_balanced_split_planning_on_the_mfma_family():
-    """partition_size=0 on bf16 GQA: the balanced split over W resident
-    one-wave workgroups (runs); the workspace holds (units + W) slots of
-    group_size rows."""
+    """partition_size=0 on bf16 GQA: the balanced split, unit-parallel (the
+    8 units of a request are the 8 waves of each workgroup, walking the same
+    request tiles), over W resident workgroups (runs); the workspace holds
+    (requests x unit groups + W) slots of 8 units x group_size rows."""
     lib = _lib.load()
     a = _args(partition_size=0, max_context_len=8192)
     part = lib.ikl_paged_attention_partition_size(ctypes.byref(a))
     ws = lib.ikl_paged_attention_workspace_size(ctypes.byref(a))
-    units, group, tiles = 32 * 8, 4, 32 * 8 * 512
+    units, group, tiles, uw = 32 * 8, 4, 32 * 8 * 512, 8
+    seq = tiles // uw  # (request, unit group, tile) entries
     assert part > 0 and part % 16 == 0
-    runs = -(-tiles // (part // 16))  # lower bound on W from the longest run
-    assert ws >= (units + runs) * group * (128 * 4 + 4)
+    runs = -(-seq // (part // 16))  # lower bound on W from the longest run
+    assert ws >= (units // uw + runs) * uw * group * (128 * 4 + 4)
     cfg = ops.launch_config(a)
-    assert (cfg["split"], cfg["num_warps"]) == ("balanced", 1)
+    assert (cfg["split"], cfg["num_warps"]) == ("balanced", uw)
     if not torch.cuda.is_available():  # planning without a device assumes 256 CUs x 8 waves
-        assert cfg["workgroups"] == 2048
-        assert part == 16 * (tiles // 2048)
-        rows = (units + 2048) * group
+        assert cfg["workgroups"] == 256
+        assert part == 16 * (seq // 256)
+        rows = (units // uw + 256) * uw * group
         assert ws == -(-(rows * 128 * 4) // 256) * 256 + rows * 4
 
 
@@ -146,9 +148,9 @@ def test_split_choice_by_batch_size_on_the_mfma_family():
     a = _args(partition_size=-2, max_context_len=1024, batch=2)
     part = lib.ikl_paged_attention_partition_size(ctypes.byref(a))
     assert part > 0 and part % 16 == 0 and ops.launch_config(a)["split"] == "balanced"
-    # 1024 tiles at the longest context, at least 4 tiles per one-wave run:
-    # 256 runs of 4 tiles
-    assert part == 64 and ops.launch_config(a)["workgroups"] == 256
+    # 1024 tiles at the longest context, the 8 units of a request in one
+    # workgroup: 128 (request, tile) entries, at least 4 per run: 32 runs of 4
+    assert part == 64 and ops.launch_config(a)["workgroups"] == 32
     # 32-head units run 2-wave workgroups, at least 4 tiles per wave
     a = _args(partition_size=-2, max_context_len=4096, batch=64, num_kv_heads=1)
     cfg = ops.launch_config(a)
@@ -237,14 +239,15 @@ def test_small_mha_launches_take_the_mfma_family():
 @pytest.mark.parametrize(
     ("dtype", "heads_per_kv", "partition", "expect"),
     [
-        (_lib.IKL_BF16, 4, 0, ("mfma_grouped", 16, 1, "balanced")),
+        # the balanced split runs unit-parallel: 8 units per request -> 8-wave workgroups
+        (_lib.IKL_BF16, 4, 0, ("mfma_grouped", 16, 8, "balanced")),
         (_lib.IKL_BF16, 4, 512, ("mfma_grouped", 16, 4, "fixed_partitions")),
         (_lib.IKL_BF16, 4, -1, ("mfma_grouped", 16, 4, "none")),
         (_lib.IKL_F32, 4, 0, ("scalar_grouped", None, 1, "fixed_partitions")),
         (_lib.IKL_F16, 1, 0, ("mha_fallback", None, 1, "fixed_partitions")),
         # -2 asks for the balanced split, which moves MHA to the MFMA family
-        (_lib.IKL_F16, 1, -2, ("mfma_grouped", 16, 1, "balanced")),
-        (_lib.IKL_BF16, 1, -2, ("mfma_grouped", 16, 1, "balanced")),
+        (_lib.IKL_F16, 1, -2, ("mfma_grouped", 16, 8, "balanced")),
+        (_lib.IKL_BF16, 1, -2, ("mfma_grouped", 16, 8, "balanced")),
     ],
 )
 def test_launch_config_reports_the_resolved_launch(dtype, heads_per_kv, partition, expect):

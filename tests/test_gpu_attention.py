@@ -193,7 +193,9 @@ def test_repeat_runs_are_bit_identical():
 # ---------------------------------------------------------------- balanced split
 # partition_size=-2 runs the MFMA family's balanced split (None picks it for
 # batches above 32768 tiles): the batch's tiles are cut into one equal run
-# per workgroup (one wave for units of up to 16 heads; 2 waves for 32-head
+# per workgroup (for units of up to 16 heads, groups of 2, 4 or 8 units of a
+# request as the waves of one workgroup walking the same request tiles, or
+# one-wave runs when the units per request are odd; 2 waves for 32-head
 # units, which share each piece of the run and merge it in LDS), and the
 # pieces are merged per unit by the reduce.
 
@@ -479,7 +481,8 @@ def test_autotune_reporters_describe_the_last_launch():
     ops.paged_decode_attention_hip(case.device_query(), case.device_cache(), case.device_tables(),
                                    case.device_lengths(), partition_size=-2)
     cfg = ops.paged_decode_grouped_dot_autotune_config()
-    assert cfg == {"block_n": 16, "num_warps": 1, "num_stages": 2}  # the balanced split: one-wave runs
+    # the balanced split, unit-parallel: the request's 2 units are the 2 waves of a workgroup
+    assert cfg == {"block_n": 16, "num_warps": 2, "num_stages": 2}
     case32 = make_case(batch=2, num_heads=8, num_kv_heads=8, head_dim=64, block_size=16,
                        lengths=[30, 40], dtype="float32", seed=51)
     ops.paged_decode_attention_hip(case32.device_query(), case32.device_cache(), case32.device_tables(),
@@ -558,3 +561,34 @@ def test_nan_key_inside_the_context_propagates_like_the_reference(dtype, heads, 
     finite = ~np.isnan(expected)
     assert finite.sum() == expected.size - per_kv * 64
     assert np.abs(got[finite] - expected[finite]).max() <= ATOL[dtype]
+
+
+@pytest.mark.parametrize(("heads", "kv", "qgs", "dim", "waves"), [
+    (32, 8, 0, 128, 8),   # 8 units per request: one 8-wave group
+    (16, 16, 0, 64, 8),   # MHA on the matrix cores: 16 one-head units, two 8-unit groups
+    (32, 4, 2, 128, 8),   # query groups of 2: 16 units, two groups
+    (12, 6, 0, 64, 2),    # 6 units: three 2-unit groups
+    (8, 2, 0, 32, 2),     # 2 units
+    (24, 3, 0, 128, 1),   # 3 units: one-unit runs
+])
+def test_balanced_split_unit_parallel_workgroups(heads, kv, qgs, dim, waves):
+    """The balanced split's unit-parallel form: each workgroup's waves are
+    consecutive units of a request walking the same request tiles, so the
+    sequence is (request, unit group, tile) and the reduce finds a unit's
+    pieces at stride UW. Ragged lengths (1, block edges, long) over 9
+    requests, against the oracle; the launch reports UW waves per group."""
+    from inferkernellab_amd import ops
+
+    lengths = [1, 16, 17, 700, 2047, 33, 300, 1024, 5]
+    case = make_case(batch=9, num_heads=heads, num_kv_heads=kv, head_dim=dim, block_size=16,
+                     lengths=lengths, dtype="bfloat16", seed=heads + kv + dim)
+    fn = "paged_decode_attention_hip_grouped" if qgs else "paged_decode_attention_hip"
+    kw = {"query_group_size": qgs} if qgs else {}
+    _check(case, fn, label=f"unit-parallel-{waves}", partition_size=-2, **kw)
+    attn = ops.PreparedPagedAttention(case.device_query(), case.device_cache(), case.device_tables(),
+                                      case.device_lengths(), max_context_len=max(lengths), partition_size=-2,
+                                      query_group_size=qgs)
+    assert attn.balanced_split and attn.launch["num_warps"] == waves
+    out = attn()
+    torch.cuda.synchronize()
+    assert max_abs_err(out, case.expected()) <= ATOL["bfloat16"]
