@@ -335,14 +335,14 @@ int ikl_paged_attention_noalloc(const ikl_paged_attention_args *args, void *stre
  * paged decode attention over context_lens, then the KV append of the
  * step's new rows. When the attention splits (a reduce kernel runs) and the
  * append is a plain copy in 16-byte pieces (16-bit or fp32 cache, aligned
- * rows of at most 512 bytes), the reduce kernel's workgroups also do the
- * append: one launch less per step, with the same result as
- * ikl_paged_attention followed by ikl_append_kv (the reduce runs after the
- * attention kernel has read the cache). Otherwise the two run as separate
- * launches in that order. Both argument structs are validated before
- * anything is enqueued, except an FP8 append's own checks, which run after
- * the attention has been enqueued. No counterpart in the reference, which
- * launches the two operators separately. */
+ * rows of at most 512 bytes) or a quantising append into an FP8 cache whose
+ * key / value rows are in the attention's dtype, the reduce kernel's
+ * workgroups also do the append: one launch less per step, with the same
+ * result as ikl_paged_attention followed by ikl_append_kv, codes and scales
+ * included (the reduce runs after the attention kernel has read the cache).
+ * Otherwise the two run as separate launches in that order. Both argument
+ * structs are validated before anything is enqueued. No counterpart in the
+ * reference, which launches the two operators separately. */
 int ikl_paged_decode_step(const ikl_paged_attention_args *attention, const ikl_append_args *append,
                           void *stream);
 

@@ -9,6 +9,7 @@
 // contiguous cache memory per instruction instead of one head_dim row per
 // program. Slots outside the cache are skipped (the reference's Triton
 // kernel has no bound check, append.py:44-66).
+#include "fp8_row.h"
 #include "ikl_common.h"
 #include "paged_attn.h"
 
@@ -99,41 +100,6 @@ struct Fp8AppendParams {
   int32_t head_dim;
 };
 
-template <typename Tag>
-__device__ inline void load4(const char *p, float *x);
-template <>
-__device__ inline void load4<bf16_tag>(const char *p, float *x) {
-  const uint2 w = *reinterpret_cast<const uint2 *>(p);
-  x[0] = elem<bf16_tag>::lo(w.x);
-  x[1] = elem<bf16_tag>::hi(w.x);
-  x[2] = elem<bf16_tag>::lo(w.y);
-  x[3] = elem<bf16_tag>::hi(w.y);
-}
-template <>
-__device__ inline void load4<f16_tag>(const char *p, float *x) {
-  const uint2 w = *reinterpret_cast<const uint2 *>(p);
-  x[0] = elem<f16_tag>::lo(w.x);
-  x[1] = elem<f16_tag>::hi(w.x);
-  x[2] = elem<f16_tag>::lo(w.y);
-  x[3] = elem<f16_tag>::hi(w.y);
-}
-template <>
-__device__ inline void load4<f32_tag>(const char *p, float *x) {
-  const float4 w = *reinterpret_cast<const float4 *>(p);
-  x[0] = w.x;
-  x[1] = w.y;
-  x[2] = w.z;
-  x[3] = w.w;
-}
-
-__device__ inline float wave_max(float v) {
-  v = fmaxf(v, dpp_mov<DPP_QUAD_XOR1>(v));
-  v = fmaxf(v, dpp_mov<DPP_QUAD_XOR2>(v));
-  v = fmaxf(v, dpp_mov<DPP_ROW_HALF_MIRROR>(v));
-  v = fmaxf(v, dpp_mov<DPP_ROW_MIRROR>(v));
-  return max_xor32(max_xor16(v));
-}
-
 template <typename Tag, typename IdxT>
 __global__ __launch_bounds__(64) void append_kv_fp8_kernel(Fp8AppendParams p) {
   constexpr int EB = elem<Tag>::bytes;
@@ -149,23 +115,17 @@ __global__ __launch_bounds__(64) void append_kv_fp8_kernel(Fp8AppendParams p) {
   const int64_t slot = (int64_t)reinterpret_cast<const IdxT *>(p.slots)[t];
   asm volatile("" ::"v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]));
   if (slot < 0 || slot >= p.num_slots) return;
-  if (!on) x[0] = x[1] = x[2] = x[3] = 0.f;
   const int64_t blk = slot / p.block_size;
   const int64_t off = slot - blk * p.block_size;
-  const float amax = wave_max(fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))));
-  const float scale = e4m3_row_scale(amax);
-  float y[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) y[i] = fminf(fmaxf(x[i] / scale, -448.0f), 448.0f);
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
-  w = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w, true);
-  if (on) *reinterpret_cast<int *>(p.dst[which] + blk * p.dst_sb[which] + off * p.dst_st[which] + h * p.dst_sh[which] + 4 * lane) = w;
-  if (lane == 0) p.scale[which][blk * p.scale_sb + h * p.scale_sh + off] = scale;
+  store_fp8_row(p.dst[which] + blk * p.dst_sb[which] + off * p.dst_st[which] + h * p.dst_sh[which],
+                p.scale[which] + blk * p.scale_sb + h * p.scale_sh + off, lane, on, x);
 }
 
 bool aligned(const void *ptr, int64_t n) { return ((uintptr_t)ptr % (uintptr_t)n) == 0; }
 
-int append_fp8(const ikl_append_args *a, hipStream_t s) {
+// Validates an FP8 append and fills its launch parameters (IKL_OK or an
+// IKL_E* code with the message set).
+int fp8_params(const ikl_append_args *a, Fp8AppendParams &p) {
   int eb;
   switch (a->dtype) {
     case IKL_F16:
@@ -176,7 +136,6 @@ int append_fp8(const ikl_append_args *a, hipStream_t s) {
   if (a->head_dim % 4 != 0 || a->head_dim > 256)
     return fail(IKL_EUNSUPPORTED, "append: the FP8 cache needs head_dim a multiple of 4, at most 256");
   if (!a->k_scale || !a->v_scale) return fail(IKL_EINVAL, "append: the FP8 cache needs k_scale and v_scale");
-  Fp8AppendParams p;
   p.src[0] = (const char *)a->key;
   p.src[1] = (const char *)a->value;
   p.src_st[0] = a->key_stride_t * eb;
@@ -210,6 +169,13 @@ int append_fp8(const ikl_append_args *a, hipStream_t s) {
       !aligned(a->v_cache, 4) || !aligned(a->k_scale, 4) || !aligned(a->v_scale, 4))
     return fail(IKL_EINVAL, "append: misaligned tensor pointer");
   if ((int64_t)a->num_kv_heads * 2 > 0x7fffffffLL) return fail(IKL_EINVAL, "append: too many heads");
+  return IKL_OK;
+}
+
+int append_fp8(const ikl_append_args *a, hipStream_t s) {
+  Fp8AppendParams p;
+  const int rc = fp8_params(a, p);
+  if (rc != IKL_OK) return rc;
   const dim3 grid((unsigned)(2 * a->num_kv_heads), (unsigned)a->num_tokens);
 #define IKL_FP8_LAUNCH(TAG, IDX) append_kv_fp8_kernel<TAG, IDX><<<grid, 64, 0, s>>>(p)
   const bool i32 = a->slot_type == IKL_I32;
@@ -299,7 +265,40 @@ int prepare_fused_append(const ikl_append_args *a, FusedAppend &f) {
   f = FusedAppend{};
   const int rc = check_append(a);
   if (rc != IKL_OK || a->num_tokens == 0) return rc;
-  if (a->cache_dtype == IKL_FP8_E4M3) return 1;
+  if (a->cache_dtype == IKL_FP8_E4M3) {
+    // quantised rows, one reduce workgroup (one wave) per (token, head, K or V)
+    Fp8AppendParams q;
+    const int qrc = fp8_params(a, q);
+    if (qrc != IKL_OK) return qrc;
+    f.fp8 = 1;
+    f.src_dtype = a->dtype;
+    f.head_dim = a->head_dim;
+    f.key = q.src[0];
+    f.value = q.src[1];
+    f.key_st = q.src_st[0];
+    f.key_sh = q.src_sh[0];
+    f.value_st = q.src_st[1];
+    f.value_sh = q.src_sh[1];
+    f.slots = q.slots;
+    f.kc = q.dst[0];
+    f.vc = q.dst[1];
+    f.kc_sb = q.dst_sb[0];
+    f.kc_st = q.dst_st[0];
+    f.kc_sh = q.dst_sh[0];
+    f.vc_sb = q.dst_sb[1];
+    f.vc_st = q.dst_st[1];
+    f.vc_sh = q.dst_sh[1];
+    f.k_scale = q.scale[0];
+    f.v_scale = q.scale[1];
+    f.s_sb = q.scale_sb;
+    f.s_sh = q.scale_sh;
+    f.rows = a->num_tokens * (int64_t)a->num_kv_heads;
+    f.num_slots = q.num_slots;
+    f.kv_heads = a->num_kv_heads;
+    f.block_size = a->block_size;
+    f.slots_i64 = a->slot_type == IKL_I64;
+    return IKL_OK;
+  }
   AppendParams p;
   int chunk = 0;
   const int prc = copy_params(a, p, chunk);

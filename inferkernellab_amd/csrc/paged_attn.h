@@ -16,8 +16,9 @@ constexpr float RESCALE_LOG2 = 8.0f;      // lazy-rescale threshold (factor 256)
 
 // KV append carried by the split reduce kernel (ikl_paged_decode_step): its
 // workgroups also scatter `rows` (token, kv head) rows of new K/V into the
-// cache, as ikl_append_kv does. Only for plain copies in 16-byte chunks
-// (16-bit or fp32 caches, aligned rows of at most 32 chunks).
+// cache, as ikl_append_kv does: plain copies in 16-byte chunks (16-bit or
+// fp32 caches, aligned rows of at most 32 chunks), or (fp8) rows quantised
+// into an FP8 cache, one workgroup per (token, head, K or V) row.
 struct FusedAppend {
   const char *key;
   const char *value;
@@ -32,12 +33,20 @@ struct FusedAppend {
   int32_t chunks;     // 16-byte chunks per head row, <= 32
   int32_t block_size;
   int32_t slots_i64;
+  // FP8 cache: codes into kc / vc, one fp32 scale per row into k_scale /
+  // v_scale [blocks, kv heads, block_size] (strides in elements)
+  int32_t fp8;
+  int32_t src_dtype;  // enum ikl_dtype of key / value
+  int32_t head_dim;
+  float *k_scale;
+  float *v_scale;
+  int64_t s_sb, s_sh;
 };
 
 // Fills `f` from the arguments of an ikl_append_kv call: IKL_OK when the
 // append can ride on the reduce kernel, 1 when it is valid but must run as
-// its own launch (FP8 cache, rows not 16-byte aligned or longer than 512
-// bytes), an IKL_E* code when the arguments are invalid (message set).
+// its own launch (rows not 16-byte aligned or longer than 512 bytes), an
+// IKL_E* code when the arguments are invalid (message set).
 int prepare_fused_append(const ikl_append_args *a, FusedAppend &f);
 
 struct AttnParams {

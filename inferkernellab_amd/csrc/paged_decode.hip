@@ -33,6 +33,7 @@
 #include <mutex>
 #include <string>
 
+#include "fp8_row.h"
 #include "ikl_common.h"
 #include "paged_attn.h"
 
@@ -410,6 +411,44 @@ __device__ inline FusedRow fused_append_load(const FusedAppend &f, int64_t row0,
   return r;
 }
 
+// FP8 cache: row r of the 2 x rows (token, head, K or V) rows, one wave per
+// row, loaded when the kernel starts and quantised after the partials are
+// read (store_fp8_row, as ikl_append_kv writes it).
+struct Fp8FusedRow {
+  float x[4];
+  int64_t slot, t;
+  int h, which;
+  bool valid, on;
+};
+
+template <typename Tag>
+__device__ inline Fp8FusedRow fused_fp8_load(const FusedAppend &f, int64_t r, int lane) {
+  constexpr int EB = elem<Tag>::bytes;
+  Fp8FusedRow row{};
+  row.valid = r < 2 * f.rows;
+  if (!row.valid) return row;
+  row.which = (int)(r & 1);
+  const int64_t tr = r >> 1;
+  row.t = tr / f.kv_heads;
+  row.h = (int)(tr - row.t * f.kv_heads);
+  row.on = 4 * lane < f.head_dim;
+  const char *src = row.which ? f.value + row.t * f.value_st + row.h * f.value_sh
+                              : f.key + row.t * f.key_st + row.h * f.key_sh;
+  load4<Tag>(src + (row.on ? 4 * lane * EB : 0), row.x);  // lanes past the row re-read its start
+  row.slot = f.slots_i64 ? load_index<int64_t>(f.slots, row.t) : load_index<int32_t>(f.slots, row.t);
+  return row;
+}
+
+// Every lane of the wave calls it (the row and its slot are the wave's).
+__device__ inline void fused_fp8_store(const FusedAppend &f, const Fp8FusedRow &r, int lane) {
+  if (!r.valid || r.slot < 0 || r.slot >= f.num_slots) return;  // slots outside the cache are skipped
+  const int64_t blk = r.slot / f.block_size, off = r.slot - blk * f.block_size;
+  char *dst = r.which ? f.vc + blk * f.vc_sb + off * f.vc_st + r.h * f.vc_sh
+                      : f.kc + blk * f.kc_sb + off * f.kc_st + r.h * f.kc_sh;
+  float *scale = (r.which ? f.v_scale : f.k_scale) + blk * f.s_sb + r.h * f.s_sh + off;
+  store_fp8_row(dst, scale, lane, r.on, r.x);
+}
+
 __device__ inline void fused_append_store(const FusedAppend &f, const FusedRow &r) {
   if (!r.on || r.slot < 0 || r.slot >= f.num_slots) return;  // slots outside the cache are skipped
   const int64_t blk = r.slot / f.block_size, off = r.slot - blk * f.block_size;
@@ -436,8 +475,10 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(const AttnParam
   const int64_t b = blockIdx.y;
   // fused append: first pass loaded now, stored once the partials are in
   const int64_t wg = b * gridDim.x + hq, nwg = (int64_t)gridDim.x * gridDim.y;
-  const int64_t app_rpp = p.app.rows > 0 ? 64 / (2 * p.app.chunks) : 0;
-  const FusedRow first_row = p.app.rows > 0 ? fused_append_load(p.app, wg * app_rpp, lane) : FusedRow{};
+  const bool app8 = p.app.rows > 0 && p.app.fp8;
+  const int64_t app_rpp = p.app.rows > 0 && !app8 ? 64 / (2 * p.app.chunks) : 0;
+  const FusedRow first_row = app_rpp > 0 ? fused_append_load(p.app, wg * app_rpp, lane) : FusedRow{};
+  const Fp8FusedRow first_row8 = app8 ? fused_fp8_load<Tag>(p.app, wg, lane) : Fp8FusedRow{};
   int np;
   int64_t prow, pstride;
   if (p.sk_waves > 0) {
@@ -495,7 +536,10 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(const AttnParam
       part_m[grp] = m;
     }
   }
-  if (p.app.rows > 0) {
+  if (app8) {
+    fused_fp8_store(p.app, first_row8, lane);
+    for (int64_t r = wg + nwg; r < 2 * p.app.rows; r += nwg) fused_fp8_store(p.app, fused_fp8_load<Tag>(p.app, r, lane), lane);
+  } else if (p.app.rows > 0) {
     fused_append_store(p.app, first_row);
     for (int64_t row0 = (wg + nwg) * app_rpp; row0 < p.app.rows; row0 += nwg * app_rpp)
       fused_append_store(p.app, fused_append_load(p.app, row0, lane));
@@ -1061,7 +1105,9 @@ int step_plan(const ikl_paged_attention_args *a, const ikl_append_args *app, Pla
   if (rc != IKL_OK) return rc;
   rc = prepare_fused_append(app, f);
   if (rc < 0) return rc;
-  const bool can_fuse = rc == IKL_OK && f.rows > 0;
+  // an FP8 append rides along when its rows are in the query dtype (the
+  // reduce kernel's element type)
+  const bool can_fuse = rc == IKL_OK && f.rows > 0 && (!f.fp8 || f.src_dtype == a->dtype);
   if (alt_ws) *alt_ws = 0;
   if (can_fuse && !pl.split && pl.scalar_waves > 1) {
     Plan alt;

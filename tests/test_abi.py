@@ -491,7 +491,11 @@ def _append_args(**kw):
         ({}, {}, 1),                                   # balanced split + 16-byte rows: fused
         ({"partition_size": 512}, {}, 1),              # fixed partitions split too
         ({"partition_size": -1}, {}, 0),               # no reduce kernel: separate append
-        ({}, {"cache_dtype": _lib.IKL_FP8_E4M3}, 0),   # FP8 append quantises: separate
+        # FP8 append: quantised on the reduce as well, when its rows are in the query dtype
+        ({}, {"cache_dtype": _lib.IKL_FP8_E4M3, "k_scale": 0x60000, "v_scale": 0x70000}, 1),
+        ({}, {"cache_dtype": _lib.IKL_FP8_E4M3, "k_scale": 0x60000, "v_scale": 0x70000,
+              "dtype": _lib.IKL_F16}, 0),
+        ({}, {"cache_dtype": _lib.IKL_FP8_E4M3}, _lib.IKL_EINVAL),  # no scale tensors
         ({}, {"key": 0x10008}, 0),                     # rows only 8-byte aligned: separate
         ({}, {"num_tokens": 0}, 0),                    # nothing to append
         ({}, {"key": 0}, _lib.IKL_EINVAL),             # invalid append

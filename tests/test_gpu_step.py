@@ -123,36 +123,60 @@ def test_step_appends_more_rows_than_one_pass_covers():
     assert step.fused
 
 
-def test_step_over_the_fp8_cache_runs_the_append_separately():
+@pytest.mark.parametrize("partition,slot_dtype", [(128, torch.int32), (-2, torch.int64)])
+def test_step_over_the_fp8_cache_fuses_the_quantising_append(partition, slot_dtype):
+    """Over the FP8 cache the reduce kernel also carries the append, one
+    wave per (token, head, K or V) row quantised as ikl_append_kv does: the
+    cache codes and scales equal the separate append's and the oracle's
+    quantiser (quantize_rows_e4m3) bit for bit, the attention equals the
+    attention alone. 37 tokens x 4 heads = 296 rows over 2 x 8 reduce
+    workgroups (several passes); one slot outside the cache is skipped."""
     from inferkernellab_amd import ops
-    from inferkernellab_amd.cache import PagedKVCache
+    from inferkernellab_amd.cache import PagedKVCache, quantize_rows_e4m3
 
-    print("decode step fp8", flush=True)
-    cache = PagedKVCache(64, 16, 2, 128, dtype=torch.float8_e4m3fn, act_dtype=torch.bfloat16, device="cuda")
-    cache.k.view(torch.uint8).zero_()
-    cache.v.view(torch.uint8).zero_()
-    cache.k_scale.fill_(1.0)
-    cache.v_scale.fill_(1.0)
-    q = torch.randn(2, 8, 128, device="cuda").to(torch.bfloat16)
+    print(f"decode step fp8 fused append partition={partition}", flush=True)
+
+    def fresh():
+        c = PagedKVCache(64, 16, 4, 128, dtype=torch.float8_e4m3fn, act_dtype=torch.bfloat16, device="cuda")
+        c.k.view(torch.uint8).fill_(0x11)
+        c.v.view(torch.uint8).fill_(0x22)
+        c.k_scale.fill_(0.5)
+        c.v_scale.fill_(0.25)
+        return c
+
+    cache, ref_cache = fresh(), fresh()
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    q = torch.randn(2, 8, 128, device="cuda", generator=gen).to(torch.bfloat16)
     tables = torch.arange(64, dtype=torch.int32, device="cuda").view(2, 32)
     lens = torch.tensor([300, 200], dtype=torch.int32, device="cuda")
-    key = torch.randn(2, 2, 128, device="cuda").to(torch.bfloat16)
-    slots = torch.tensor([300, 32 * 16 + 200], dtype=torch.int32, device="cuda")
-    attn = ops.PreparedPagedAttention(q, cache, tables, lens, partition_size=128)
-    step = ops.PreparedDecodeStep(attn, ops.PreparedAppend(key, key.clone(), cache, slots))
-    assert not step.fused
+    key = (torch.randn(37, 4, 128, device="cuda", generator=gen) * 3).to(torch.bfloat16)
+    value = torch.randn(37, 4, 128, device="cuda", generator=gen).to(torch.bfloat16)
+    key[5].zero_()  # a zero row: scale 1
+    slot_list = [400 + i for i in range(36)] + [64 * 16 + 3]  # the last one is outside the cache
+    slots = torch.tensor(slot_list, dtype=slot_dtype, device="cuda")
+    attn = ops.PreparedPagedAttention(q, cache, tables, lens, partition_size=partition)
+    step = ops.PreparedDecodeStep(attn, ops.PreparedAppend(key, value, cache, slots))
+    assert step.fused and step.kernel_names()[-1] == "paged_decode_reduce_kernel"
     step()
-    ref_cache = PagedKVCache(64, 16, 2, 128, dtype=torch.float8_e4m3fn, act_dtype=torch.bfloat16, device="cuda")
-    ref_cache.k.view(torch.uint8).zero_()
-    ref_cache.v.view(torch.uint8).zero_()
-    ref_cache.k_scale.fill_(1.0)
-    ref_cache.v_scale.fill_(1.0)
-    ref = ops.paged_decode_attention_hip(q, ref_cache, tables, lens, partition_size=128)
-    ops.append_kv_hip(key, key.clone(), ref_cache, slots)
+    ref = ops.paged_decode_attention_hip(q, ref_cache, tables, lens, partition_size=partition)
+    ops.append_kv_hip(key, value, ref_cache, slots)
     torch.cuda.synchronize()
     assert torch.equal(step.out.view(torch.int16), ref.view(torch.int16))
-    assert torch.equal(cache.k.view(torch.uint8), ref_cache.k.view(torch.uint8))
-    assert torch.equal(cache.k_scale, ref_cache.k_scale)
+    for a, b in ((cache.k, ref_cache.k), (cache.v, ref_cache.v)):
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+    assert torch.equal(cache.k_scale, ref_cache.k_scale) and torch.equal(cache.v_scale, ref_cache.v_scale)
+    # against the quantiser directly, row by row
+    s = torch.tensor(slot_list[:36], device="cuda")
+    blk, off = s // 16, s % 16
+    for new, codes, scales in ((key[:36], cache.k, cache.k_scale), (value[:36], cache.v, cache.v_scale)):
+        c, sc = quantize_rows_e4m3(new)
+        assert torch.equal(codes[0][blk, off].view(torch.uint8), c.view(torch.uint8))
+        assert torch.equal(scales[0][blk, :, off], sc)
+    assert float(cache.k_scale[0][25, :, 5].min()) == 1.0  # slot 405: the zero row
+    # nothing else of the cache changed
+    untouched = torch.ones(64 * 16, dtype=torch.bool, device="cuda")
+    untouched[s] = False
+    assert (cache.k[0].reshape(64 * 16, 4, 128)[untouched].view(torch.uint8) == 0x11).all()
 
 
 def test_step_function_and_graph_replays():
