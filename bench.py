@@ -1369,8 +1369,8 @@ def read_ceiling(device: torch.device, nbytes: int = 512 << 20, samples: int = 5
         "read_median_gbps": round(nbytes / med / 1e9, 1),
         "bytes": nbytes,
         "samples": samples,
-        "kernel": "hbm_read_probe_kernel (one contiguous chunk per workgroup, 16-byte non-temporal loads, "
-                  "8 workgroups of 256 per CU)",
+        "kernel": "hbm_read_probe_kernel (one contiguous chunk per one-wave workgroup, 16-byte non-temporal "
+                  "loads, 8 waves per CU)",
     }
 
 

@@ -13,16 +13,16 @@
 namespace ikl {
 namespace {
 
-constexpr int PROBE_THREADS = 256;
+constexpr int PROBE_THREADS = 64;  // one wave per workgroup, one chunk per wave
 constexpr int PROBE_UNROLL = 4;  // 16-byte loads in flight per thread
 constexpr uint32_t PROBE_TAG = 0x9e3779b9u;
 
-// Workgroup w streams its own contiguous chunk [w n16 / G, (w + 1) n16 / G)
-// of 16-byte pieces front to back (PROBE_UNROLL loads in flight per
-// thread). Chunks per workgroup stream markedly faster than a grid-stride
-// sweep of the same buffer (6.6-6.7 against 5.1-5.9 TB/s measured on
-// MI355X for 512 MiB - 1 GiB), which interleaves every wave's loads over
-// the whole buffer.
+// Workgroup (one wave) w streams its own contiguous chunk [w n16 / G,
+// (w + 1) n16 / G) of 16-byte pieces front to back (PROBE_UNROLL loads in
+// flight per lane). On MI355X, 1 GiB: one-wave chunks at 8 waves per CU
+// read 7.06 TB/s, 256-thread chunks 6.6-6.7, and a grid-stride sweep of the
+// same buffer, which interleaves every wave's loads over all of it,
+// 5.1-5.9.
 __global__ __launch_bounds__(PROBE_THREADS) void hbm_read_probe_kernel(const v4u32 *__restrict__ src, int64_t n16,
                                                                         uint32_t *sink) {
   const int64_t lo = (int64_t)blockIdx.x * n16 / gridDim.x, hi = ((int64_t)blockIdx.x + 1) * n16 / gridDim.x;
@@ -60,8 +60,8 @@ extern "C" int ikl_hbm_read_probe(const void *buffer, int64_t bytes, void *sink,
     cus = 256;
   }
   const int64_t n16 = bytes / 16;
-  // 8 workgroups per CU (2 waves per SIMD of 4-wave groups), fewer for a
-  // buffer that cannot feed them one unrolled pass each
+  // 8 one-wave workgroups per CU (2 waves per SIMD), fewer for a buffer
+  // that cannot feed them one unrolled pass each
   const int64_t want = (n16 + PROBE_THREADS * PROBE_UNROLL - 1) / (PROBE_THREADS * PROBE_UNROLL);
   const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(want, (int64_t)cus * 8));
   if (sink_bytes < grid * 4)
