@@ -21,12 +21,16 @@ kernel with HIP events recorded around it on its stream; ``cpu_baseline``
 times the CPU oracle (a numpy restatement of paged_reference) on a bounded
 sample of the same requests.
 
-Workloads whose step K/V is below 512 MiB (everything but the default) fit
-in the 256 MB MALL, so by default (``--mall-flush auto``) a 512 MiB buffer
-is read before every timed sample (a read, so that no dirty lines are left
-to write back during the sample): outside the HIP-event brackets of the
-kernels, and its own event-timed duration is taken out of the step's wall
-time.
+Workloads whose step K/V is below 384 MiB (1.5x the 256 MB MALL) could be
+served in part from the MALL when steps run back to back, so by default
+(``--mall-flush auto``) a 512 MiB buffer is read before every timed sample
+of those (a read, so that no dirty lines are left to write back during the
+sample): outside the HIP-event brackets of the kernels, and its own
+event-timed duration is taken out of the step's wall time. Above that the
+steps run back to back with no flush: the GQA decode shape over the FP8
+cache (414 MB of K/V) measured its attention kernel at 75.7-77.1 us back to
+back and 72.9-73.0 us with a flush before every step, so the MALL serves it
+nothing.
 
 ``--workload prefill_*`` measures the paged prefill attention kernel
 instead (one causal launch over a batch of prompt chunks): ``value`` and
@@ -69,6 +73,11 @@ WORKLOADS = {
     "mqa32x1_hd64_bf16_b16_ctx2k": (16, 32, 1, 64, torch.bfloat16, 2048, 2048, None, 1.0, None),
 }
 DEFAULT_WORKLOAD = "gqa32x8_hd128_bf16_b32_ctx4k-8k"
+
+
+# Steps whose K/V is below this many bytes get a MALL flush before every
+# timed sample (1.5x the 256 MB MALL; see the module docstring).
+MALL_FLUSH_BELOW = 384 << 20
 
 
 class HipEvents:
@@ -972,7 +981,7 @@ def measure_decode(workload: str, device: torch.device, *, steps: int, warmup: i
     events = HipEvents()
     ev = [[events.create() for _ in range(3)] for _ in range(steps)]
     attn_bytes, append_bytes = step_bytes(w)
-    flush = mall_flush == "on" or (mall_flush == "auto" and attn_bytes < (512 << 20))
+    flush = mall_flush == "on" or (mall_flush == "auto" and attn_bytes < MALL_FLUSH_BELOW)
     flush_buf = MallFlush(device) if flush else None
     flush_marks = []
 
@@ -1456,7 +1465,7 @@ def main() -> int:
     parser.add_argument("--mall-flush", choices=("auto", "on", "off"), default="auto",
                         help="read a 512 MiB buffer before every timed sample so that the K/V of "
                              "the step is not served from the 256 MB MALL (auto: when the step's "
-                             "K/V is below 512 MiB, i.e. every workload but the 805 MB GQA one)")
+                             "K/V is below 384 MiB, 1.5x the MALL)")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="run only a plain 512 MiB device copy (torch copy_) three times: the "
                              "known-size reference for scaling FETCH_SIZE / WRITE_SIZE counters")
