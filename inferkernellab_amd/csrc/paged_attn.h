@@ -93,6 +93,12 @@ struct AttnParams {
   // of (request b, group ug) that run w covers lands in slots ((b * units /
   // UW + ug) + w) * UW + i.
   int32_t sk_unitw;
+  // Entries each (request, unit group) segment of the sequence counts
+  // before its first tile (0 = none): a run pays a restart at every
+  // segment it enters, so runs that cross into a segment get that many
+  // fewer tiles. Segment of a request with n > 0 tiles: n + sk_seg_cost
+  // entries, tile t at entry sk_seg_cost + t.
+  int32_t sk_seg_cost;
   int32_t grid_spread;     // fixed-partition MFMA grid is request-fastest (spread_grid)
   int64_t batch;
   int64_t cap_tokens;      // table_width * block_size: positions a table can map
@@ -198,6 +204,12 @@ __device__ inline int wave_incl_scan(int x, int lane) {
 // before b (*before), of b itself (*own) and of the whole batch (return),
 // in request-tile units (multiply by p.units for global tiles). The host
 // bounds cap_tokens so that a 64-request chunk sum fits in 32 bits.
+// Segment entries of a request with n tiles in the balanced split's
+// sequence (see AttnParams::sk_seg_cost).
+__device__ inline int seg_len(const AttnParams &p, int n) { return n > 0 ? n + p.sk_seg_cost : 0; }
+
+// Balanced split: segment entries of all requests (returned), of the
+// requests before b (*before) and request b's tiles (*own).
 __device__ inline int64_t request_tiles(const AttnParams &p, int64_t b, int lane, int64_t *before,
                                         int *own) {
   int64_t base = 0, total = 0;
@@ -206,11 +218,11 @@ __device__ inline int64_t request_tiles(const AttnParams &p, int64_t b, int lane
   for (int64_t c0 = 0; c0 < p.batch; c0 += 64) {
     const int64_t r = c0 + lane;
     const int n = r < p.batch ? (int)((clamped_ctx(p, r) + 15) >> 4) : 0;
-    const int incl = wave_incl_scan(n, lane);
+    const int incl = wave_incl_scan(seg_len(p, n), lane);
     if (b >= c0 && b < c0 + 64) {
       const int l = (int)(b - c0);
       *own = __shfl(n, l, 64);
-      *before = base + __shfl(incl, l, 64) - *own;
+      *before = base + __shfl(incl, l, 64) - seg_len(p, *own);
     }
     base += __builtin_amdgcn_readlane(incl, 63);
   }

@@ -495,7 +495,7 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(const AttnParam
     const int kvh = (int)(hq / p.heads_per_kv), r = (int)(hq % p.heads_per_kv);
     const int64_t u = (int64_t)kvh * p.groups_per_kv + r / p.group_size;
     const int64_t ug = u / UW, ui = u - ug * UW;
-    const int64_t s = NUG * before + ug * own;  // first sequence entry of the group
+    const int64_t s = NUG * before + ug * seg_len(p, own) + p.sk_seg_cost;  // the group's first tile's entry
     const int64_t w_lo = own > 0 ? wave_of_tile(s, T, W) : 0;
     const int64_t w_hi = own > 0 ? wave_of_tile(s + own - 1, T, W) : -1;
     np = (int)(w_hi - w_lo + 1);
@@ -589,6 +589,7 @@ struct Plan {
   bool split = false;
   int sk_waves = 0;  // balanced split (MFMA family): runs (workgroups) sharing the batch's tiles
   int sk_unitw = 1;  // units per balanced-split workgroup (unit-parallel form when > 1)
+  int sk_seg_cost = 0;  // leading entries per (request, unit group) segment of the balanced split
   int64_t units = 0;  // kv heads x query groups per request
   int64_t ws_o_bytes = 0;
   int64_t ws_bytes = 0;
@@ -730,6 +731,7 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl, bool fold_waves = tru
   // 64-request chunk of tile counts to fit in 32 bits (cap < 2^29 tokens)
   // and (T + 1) * W to fit in 63 bits.
   constexpr int64_t SK_MIN_BATCH_TILES = 32768;
+  constexpr int SK_SEG_COST_32 = 16, SK_SEG_COST_ONE = 4, SK_SEG_COST_UNITS = 1;
   if (a->partition_size == -2 && pl.path != IKL_PATH_MFMA_GROUPED)
     return fail(IKL_EUNSUPPORTED, "partition_size -2 (the balanced split) needs the MFMA kernel family");
   const int64_t t_max = units * ((maxctx + 15) / 16);
@@ -759,9 +761,23 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl, bool fold_waves = tru
     const int64_t w =
         std::min<int64_t>(mfma_streamk_capacity(a->dtype, a->head_dim, pl.group_size, pl.kv_fp8, uw),
                           std::max<int64_t>((t_seq + SK_MIN_TILES * skw - 1) / (SK_MIN_TILES * skw), 1));
-    if ((double)(t_seq + 1) * (double)w < 4.0e18) {
+    // A run that enters a segment of the sequence pays a restart (its
+    // epilogue, then a pipeline fill from the new request's blocks): each
+    // segment counts that many leading entries, so such runs take fewer
+    // tiles. On MQA 32/1 hd128 bf16 (32-head units, two-wave runs) runs
+    // crossing a request ended 3.7 us after the others at no cost; the
+    // kernel, with costs 0 / 4 / 8 / 16 / 20: B64 x U[1024, 4096] 28.4 /
+    // 26.8 / 25.4 / 24.9 / 25.3 us, B128 x U[1024, 4096] 40.4 (4) / 39.3 /
+    // 38.4 us, B48 x U[4096, 8192] 36.7 (4) / 35.1 / 35.1 us. Unit-parallel
+    // runs (one entry streams UW tiles) and 16-head one-unit runs move
+    // within noise (GQA 32/8 B32 x U[4096, 8192] 126.0-126.5 us at 0, 125.3-
+    // 125.9 at 1; GQA 48/3 B32 x U[4096, 8192] 60.0-60.2 us at 4 / 8 / 16).
+    const int seg_cost = uw > 1 ? SK_SEG_COST_UNITS : (pl.group_size > 16 ? SK_SEG_COST_32 : SK_SEG_COST_ONE);
+    const int64_t t_virt = t_seq + (int64_t)seg_cost * a->batch * (pl.units / uw);
+    if ((double)(t_virt + 1) * (double)w < 4.0e18) {
       pl.sk_waves = (int)w;
       pl.sk_unitw = uw;
+      pl.sk_seg_cost = seg_cost;
       pl.split = true;
       pl.num_parts = 1;
       pl.partition = (int)std::min<int64_t>(16 * ((t_seq + w - 1) / w), 0x7fffffffLL);
@@ -1056,6 +1072,7 @@ int run_attention(const ikl_paged_attention_args *a, const Plan &pl, const Fused
   p.scale_log2 = a->scale * LOG2E;
   p.sk_waves = pl.sk_waves;
   p.sk_unitw = pl.sk_unitw;
+  p.sk_seg_cost = pl.sk_seg_cost;
   p.units = (int32_t)pl.units;
   p.grid_spread = pl.path == IKL_PATH_MFMA_GROUPED && pl.sk_waves == 0 && spread_grid(pl.units, pl.num_parts, a->batch);
   p.batch = a->batch;

@@ -547,11 +547,13 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
 
 // Start of balanced-split run w: the batch's total tiles T (units x
 // request tiles), the run [g0, g1) = [w T / W, (w + 1) T / W) with W =
-// min(sk_waves, T), and the request b holding tile g0 with its tile count nb
-// and the tiles pb of the requests before it. Every lane of the calling
+// min(sk_waves, T), and the request b holding tile g0 with its clamped
+// length ctx, its tile count nb and the tiles pb of the requests before it
+// (all from one scan of the lengths). Every lane of the calling
 // wave gets the same values; `active` is false for runs past W.
 struct SkRun {
-  int64_t g0, g1, b, pb;
+  int64_t g0, g1, b, pb, ctx;
+  int64_t lane_ctx;  // batches of up to 64 requests: lane q holds request q's clamped length
   int nb;
   bool active;
 };
@@ -568,15 +570,17 @@ __device__ __forceinline__ int64_t uniform64(int64_t x) {
 }
 
 __device__ __forceinline__ SkRun sk_run(const AttnParams &p, int64_t w, int lane) {
-  SkRun r{0, 0, -1, 0, 0, false};
+  SkRun r{0, 0, -1, 0, 0, 0, 0, false};
   const int64_t U = p.units / p.sk_unitw;  // sequence entries per request tile
-  // total tiles, then the request holding the run's first tile (a batch
-  // of up to 64 requests takes one scan for both)
-  int64_t total;
+  // total sequence entries, then the request holding the run's first entry
+  // (a batch of up to 64 requests takes one scan for both); pb counts the
+  // entries of the requests before b
+  int64_t total, c1 = 0;
   int n1 = 0, incl1 = 0;
   if (p.batch <= 64) {
-    n1 = lane < p.batch ? (int)((clamped_ctx(p, lane) + 15) >> 4) : 0;
-    incl1 = wave_incl_scan(n1, lane);
+    c1 = lane < p.batch ? clamped_ctx(p, lane) : 0;
+    n1 = (int)((c1 + 15) >> 4);
+    incl1 = wave_incl_scan(seg_len(p, n1), lane);
     total = __builtin_amdgcn_readlane(incl1, 63);
   } else {
     int64_t before0;
@@ -595,19 +599,23 @@ __device__ __forceinline__ SkRun sk_run(const AttnParams &p, int64_t w, int lane
     const int l = __builtin_ctzll(hit);  // g0 < T: some request's tiles end past it
     r.b = l;
     r.nb = __shfl(n1, l, 64);
-    r.pb = __shfl(incl1, l, 64) - r.nb;
+    r.pb = __shfl(incl1, l, 64) - seg_len(p, r.nb);
+    r.ctx = ((int64_t)__shfl((int)(c1 >> 32), l, 64) << 32) | (uint32_t)__shfl((int)c1, l, 64);
+    r.lane_ctx = c1;
   }
   int64_t base = 0;
   for (int64_t c0 = 0; c0 < p.batch && r.b < 0; c0 += 64) {
     const int64_t q = c0 + lane;
-    const int n = q < p.batch ? (int)((clamped_ctx(p, q) + 15) >> 4) : 0;
-    const int incl = wave_incl_scan(n, lane);
+    const int64_t c = q < p.batch ? clamped_ctx(p, q) : 0;
+    const int n = (int)((c + 15) >> 4);
+    const int incl = wave_incl_scan(seg_len(p, n), lane);
     const uint64_t hit = __builtin_amdgcn_ballot_w64(q < p.batch && U * (base + incl) > r.g0);
     if (hit) {
       const int l = __builtin_ctzll(hit);
       r.b = c0 + l;
       r.nb = __shfl(n, l, 64);
-      r.pb = base + __shfl(incl, l, 64) - r.nb;
+      r.pb = base + __shfl(incl, l, 64) - seg_len(p, r.nb);
+      r.ctx = ((int64_t)__shfl((int)(c >> 32), l, 64) << 32) | (uint32_t)__shfl((int)c, l, 64);
     }
     base += __shfl(incl, 63, 64);
   }
@@ -615,38 +623,42 @@ __device__ __forceinline__ SkRun sk_run(const AttnParams &p, int64_t w, int lane
   r.g1 = uniform64(r.g1);
   r.b = uniform64(r.b);
   r.pb = uniform64(r.pb);
+  r.ctx = uniform64(r.ctx);
   r.nb = __builtin_amdgcn_readfirstlane(r.nb);
   return r;
 }
 
 // Moves a run to the next request with tiles after finishing request b's
-// last unit (one exists while the run has tiles left).
-__device__ __forceinline__ void sk_next_request(const AttnParams &p, int64_t &b, int &nb, int64_t &pb) {
-  do {
-    pb += nb;
-    ++b;
-    nb = __builtin_amdgcn_readfirstlane((int)((clamped_ctx(p, b) + 15) >> 4));
-  } while (nb == 0);
-}
-
-// sk_next_request, also handing back the new request's clamped length.
+// last unit (one exists while the run has tiles left), handing back the new
+// request's clamped length.
+// lane_ctx: the run's per-lane lengths from its scan (batches of up to 64
+// requests), read across lanes instead of loaded again.
 __device__ __forceinline__ void sk_next_request_ctx(const AttnParams &p, int64_t &b, int &nb, int64_t &pb,
-                                                    int64_t &ctx) {
+                                                    int64_t &ctx, int64_t lane_ctx) {
   do {
-    pb += nb;
+    pb += seg_len(p, nb);
     ++b;
-    ctx = uniform64(clamped_ctx(p, b));
+    if (p.batch <= 64)
+      ctx = uniform64(((int64_t)__shfl((int)(lane_ctx >> 32), (int)b, 64) << 32) |
+                      (uint32_t)__shfl((int)lane_ctx, (int)b, 64));
+    else
+      ctx = uniform64(clamped_ctx(p, b));
     nb = (int)((ctx + 15) >> 4);
   } while (nb == 0);
 }
 
 // Balanced split: p.sk_waves runs, one workgroup of WAVES waves each
-// (grid.x). Workgroup w attends global tiles [w T / W, (w + 1) T / W) of the
-// batch (T = units x tiles of all requests, W = min(sk_waves, T)) piece by
-// piece — a piece is the part of one (request, unit) inside the run. Its
-// waves take equal (+-1) shares of each piece's tiles and merge them in LDS,
-// as the fixed partitions' workgroups do, and the piece's normalised output
-// and log2-sum-exp go to partial slot unit + w.
+// (grid.x). Workgroup w takes entries [w T / W, (w + 1) T / W) of the
+// batch's sequence (T entries: per request and unit a segment of
+// p.sk_seg_cost leading entries and then its tiles; W = min(sk_waves, T))
+// piece by piece — a piece is the part of one (request, unit) segment
+// inside the run, and a run that ends among a segment's leading entries
+// has no piece there. Its waves take equal (+-1) shares of each piece's
+// tiles and merge them in LDS, as the fixed partitions' workgroups do, and
+// the piece's normalised output and log2-sum-exp go to partial slot unit +
+// w. As in the unit-parallel kernel below, the next piece's length and
+// table window load while a piece runs, and its Q loads behind its first
+// tile.
 template <typename Tag, int D, int NG, int WAVES, bool KV8>
 __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_streamk_kernel(const AttnParams p) {
   static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4, "1, 2 or 4 waves per workgroup");
@@ -673,23 +685,55 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
   WT wt(p);
   float *const stage = reinterpret_cast<float *>(lds);
   int64_t g = g0;
+  int64_t ctx = run.ctx;
+  int win = 0;
+  bool have_win = false;
+  const int64_t c = p.sk_seg_cost;
   while (true) {
-    // piece: unit u of request b, request tiles [t_in, t_hi)
+    // piece: unit u of request b, segment entries [v_in, v_hi), request
+    // tiles [t_in, t_hi)
+    const int64_t sl = seg_len(p, nb);
     const int64_t rel = g - U * pb;
-    const int u = (int)(rel / nb);
-    const int64_t t_in = rel - (int64_t)u * nb;
-    const int64_t t_hi = (int64_t)nb < t_in + (g1 - g) ? (int64_t)nb : t_in + (g1 - g);
+    const int u = (int)(rel / sl);
+    const int64_t v_in = rel - (int64_t)u * sl;
+    const int64_t v_hi = sl < v_in + (g1 - g) ? sl : v_in + (g1 - g);
+    const int64_t t_in = v_in > c ? v_in - c : 0, t_hi = v_hi > c ? v_hi - c : 0;
     const int kvh = u / p.groups_per_kv, qg = u % p.groups_per_kv;
     const int head0 = qg * p.group_size;
     const int nh = p.group_size < p.heads_per_kv - head0 ? p.group_size : p.heads_per_kv - head0;
     const int64_t hq0 = (int64_t)kvh * p.heads_per_kv + head0;
-    const int64_t ctx = clamped_ctx(p, b);
     // this wave's share of the piece: tiles [a0, a1), positions [a0 * 16, e)
     const int64_t n = t_hi - t_in;
     const int64_t a0 = t_in + wave * n / WAVES, a1 = t_in + (wave + 1) * n / WAVES;
     const int64_t e = a1 * TILE < ctx ? a1 * TILE : ctx;
-    wt.load_q(p, b, hq0, nh);
-    wt.attend(p, b, kvh, a0 * TILE, a1 > a0 ? e : a0 * TILE, lds + wave * WT::TILE_BYTES);
+    // the run's next piece starts at tile 0 of unit u + 1, or of the next
+    // request with tiles: its length and this wave's first table window
+    // load now, and its Q loads behind its first tile (as in the
+    // unit-parallel kernel; each piece start otherwise waited out three
+    // dependent loads: MQA 32/1 hd128 bf16 B64 x U[1024, 4096], balanced
+    // split, runs crossing a request ended 4-6 us after the others)
+    const int64_t gn = g + (v_hi - v_in);
+    int64_t bn = b, pbn = pb, ctxn = ctx;
+    int nbn = nb, win_n = 0;
+    if (gn < g1) {
+      if (v_hi == sl && u == U - 1) sk_next_request_ctx(p, bn, nbn, pbn, ctxn, run.lane_ctx);  // one exists: gn < T
+      const int64_t ve = seg_len(p, nbn) < g1 - gn ? seg_len(p, nbn) : g1 - gn;
+      const int64_t nn = ve > c ? ve - c : 0;  // the next piece's tiles
+      const int64_t blk = (int64_t)(wave * nn / WAVES) * TILE;
+      win_n = load_table_window(p, bn, p.bs_shift >= 0 ? (blk >> p.bs_shift) : blk / p.block_size, lane);
+    }
+    if (n == 0) {  // the run ends inside the segment's leading entries: no tiles, no partial
+      g = gn;
+      if (g >= g1) break;
+      b = bn;
+      pb = pbn;
+      nb = nbn;
+      ctx = ctxn;
+      win = win_n;
+      have_win = true;
+      continue;
+    }
+    wt.attend(p, b, kvh, a0 * TILE, a1 > a0 ? e : a0 * TILE, lds + wave * WT::TILE_BYTES, have_win, win, hq0, nh);
 
     // combine the waves: common max M per head, rescaled sums
     float M[NG], L[NG], f[NG];
@@ -738,16 +782,22 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
     if constexpr (WAVES > 1) __syncthreads();
     else wave_lds_sync();
 
-    g += t_hi - t_in;
+    g = gn;
     if (g >= g1) break;
-    if (t_hi == nb && u == U - 1) sk_next_request(p, b, nb, pb);  // one exists: g < T
+    b = bn;
+    pb = pbn;
+    nb = nbn;
+    ctx = ctxn;
+    win = win_n;
+    have_win = true;
   }
 }
 
 // Unit-parallel balanced split: p.sk_waves workgroups of UW waves, for
 // units of up to 16 heads. The sequence is request-major, then unit group
-// (UW consecutive units), then tile; workgroup w takes the run [w T / W,
-// (w + 1) T / W) of it and its wave i attends unit ug * UW + i over each
+// (UW consecutive units: a segment of p.sk_seg_cost leading entries, then
+// its tiles); workgroup w takes the run [w T / W, (w + 1) T / W) of it and
+// its wave i attends unit ug * UW + i over each
 // piece — so the UW waves read their heads' rows of the same cache blocks
 // at about the same time (in the token-major cache those rows interleave
 // inside each block). A load-only probe of the GQA 32/8 hd128 bf16 B32 x
@@ -783,15 +833,19 @@ __global__ __launch_bounds__(64 * UW) __attribute__((amdgpu_waves_per_eu(2, 8)))
   float *const stage = reinterpret_cast<float *>(mine);
 
   WT wt(p);
-  int64_t ctx = uniform64(clamped_ctx(p, b));
+  int64_t ctx = run.ctx;
   int win = 0;
   bool have_win = false;
+  const int64_t c = p.sk_seg_cost;
   while (true) {
-    // piece: unit group ug of request b, request tiles [t_in, t_hi)
+    // piece: unit group ug of request b, segment entries [v_in, v_hi),
+    // request tiles [t_in, t_hi)
+    const int64_t sl = seg_len(p, nb);
     const int64_t rel = g - NUG * pb;
-    const int64_t ug = rel / nb;
-    const int64_t t_in = rel - ug * nb;
-    const int64_t t_hi = (int64_t)nb < t_in + (g1 - g) ? (int64_t)nb : t_in + (g1 - g);
+    const int64_t ug = rel / sl;
+    const int64_t v_in = rel - ug * sl;
+    const int64_t v_hi = sl < v_in + (g1 - g) ? sl : v_in + (g1 - g);
+    const int64_t t_in = v_in > c ? v_in - c : 0, t_hi = v_hi > c ? v_hi - c : 0;
     const int u = (int)ug * UW + wave;
     const int kvh = u / p.groups_per_kv, qg = u % p.groups_per_kv;
     const int head0 = qg * p.group_size;
@@ -800,12 +854,23 @@ __global__ __launch_bounds__(64 * UW) __attribute__((amdgpu_waves_per_eu(2, 8)))
     const int64_t e = t_hi * TILE < ctx ? t_hi * TILE : ctx;
     // the run's next piece starts at tile 0 of group ug + 1, or of the next
     // request with tiles: its length and first window load now
-    const int64_t gn = g + (t_hi - t_in);
+    const int64_t gn = g + (v_hi - v_in);
     int64_t bn = b, pbn = pb, ctxn = ctx;
     int nbn = nb, win_n = 0;
     if (gn < g1) {
-      if (t_hi == nb && ug == NUG - 1) sk_next_request_ctx(p, bn, nbn, pbn, ctxn);  // one exists: gn < T
+      if (v_hi == sl && ug == NUG - 1) sk_next_request_ctx(p, bn, nbn, pbn, ctxn, run.lane_ctx);  // one exists: gn < T
       win_n = load_table_window(p, bn, 0, lane);
+    }
+    if (t_hi == t_in) {  // the run ends inside the segment's leading entries: no tiles, no partial
+      g = gn;
+      if (g >= g1) break;
+      b = bn;
+      pb = pbn;
+      nb = nbn;
+      ctx = ctxn;
+      win = win_n;
+      have_win = true;
+      continue;
     }
     wt.template attend<true>(p, b, kvh, t_in * TILE, e, mine, have_win, win, hq0, nh);
     const float L = wt.lsum[0], M = wt.m[0];
