@@ -510,25 +510,42 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(const AttnParam
     pstride = p.num_heads;
   }
   // One pass over the partials: each group keeps its own running maximum
-  // (online softmax over its partitions), and the groups meet in LDS.
+  // (online softmax over its partitions), and the groups meet in LDS. The
+  // partials load in batches of GROUPS * K (16) with their loads issued
+  // together: indices past np read partial np - 1 again and weigh 0, so a
+  // head with up to 16 partials waits on one memory round trip (a loop of
+  // 4-way unrolled steps plus a remainder took two or three for the 9 or so
+  // of a balanced split).
+  constexpr int K = GROUPS >= 16 ? 1 : 16 / GROUPS;
   const int grp = lane / CH;
   const int ch = lane % CH;
   if (grp < GROUPS) {
     float4 a = {0.f, 0.f, 0.f, 0.f};
     float z = 0.f, m = -INFINITY;
-#pragma unroll 4
-    for (int i = grp; i < np; i += GROUPS) {
-      const float l = p.part_lse[prow + i * pstride];
-      const float4 o = reinterpret_cast<const float4 *>(p.part_o + (prow + i * pstride) * D)[ch];
-      const float mn = fmaxf(m, l);
-      const float c = mn == -INFINITY ? 1.f : fast_exp2(m - mn);  // rescale of what is summed so far
-      const float w = mn == -INFINITY ? 0.f : fast_exp2(l - mn);  // empty partitions (-inf) weigh 0
-      z = fmaf(z, c, w);
-      a.x = fmaf(w, o.x, a.x * c);
-      a.y = fmaf(w, o.y, a.y * c);
-      a.z = fmaf(w, o.z, a.z * c);
-      a.w = fmaf(w, o.w, a.w * c);
-      m = mn;
+    for (int i0 = grp; i0 < np; i0 += GROUPS * K) {
+      float lk[K];
+      float4 ok[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int i = i0 + k * GROUPS;
+        const int64_t row = prow + (int64_t)(i < np ? i : np - 1) * pstride;
+        lk[k] = p.part_lse[row];
+        ok[k] = reinterpret_cast<const float4 *>(p.part_o + row * D)[ch];
+      }
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const float l = i0 + k * GROUPS < np ? lk[k] : -INFINITY;
+        const float4 o = ok[k];
+        const float mn = fmaxf(m, l);
+        const float c = mn == -INFINITY ? 1.f : fast_exp2(m - mn);  // rescale of what is summed so far
+        const float w = mn == -INFINITY ? 0.f : fast_exp2(l - mn);  // empty partitions (-inf) weigh 0
+        z = fmaf(z, c, w);
+        a.x = fmaf(w, o.x, a.x * c);
+        a.y = fmaf(w, o.y, a.y * c);
+        a.z = fmaf(w, o.z, a.z * c);
+        a.w = fmaf(w, o.w, a.w * c);
+        m = mn;
+      }
     }
     part_sum[grp][ch] = a;
     if (ch == 0) {
