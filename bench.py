@@ -1267,7 +1267,7 @@ def c1_cpu_reference(device: torch.device, samples: int = 10, warmup: int = 2) -
     slot_mapping (the oracle's write_slots, cache.py:156-189, and the HIP
     append into the device cache, compared bit for bit). The oracle's
     paged_reference is timed over `samples` whole steps after `warmup`
-    (BASELINE: warmup plus at least 10 samples); the HIP kernel runs on the
+    (warmup plus at least 10 samples); the HIP kernel runs on the
     same inputs beside it."""
     import numpy as np
     from oracle import paged_oracle as po

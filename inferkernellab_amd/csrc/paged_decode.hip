@@ -825,7 +825,8 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl, bool fold_waves = tru
       // B4-B64 x {512, 2048, U[1024, 4096], U[4096, 8192]} (whole operation)
       // this picked the fastest fixed size on 15 of 16 shapes: B16 x
       // U[4096, 8192] 29.2 -> 26.8 us, B32 x U[1024, 4096] 28.7 -> 25.1, B64
-      // x 2048 29.3 -> 27.0, B32 x 2048 22.6 -> 22.0; C3 keeps 512.
+      // x 2048 29.3 -> 27.0, B32 x 2048 22.6 -> 22.0; B64 x U[1024, 4096] keeps
+      // 512.
       const int64_t cap_wg = mfma_streamk_capacity(a->dtype, a->head_dim, pl.group_size, pl.kv_fp8);
       P = 128;
       while (P < 512 && units * ((maxctx + P - 1) / P) > cap_wg) P *= 2;

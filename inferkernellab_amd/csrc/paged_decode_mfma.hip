@@ -803,7 +803,7 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
 // inside each block). A load-only probe of the GQA 32/8 hd128 bf16 B32 x
 // U[4096, 8192] pattern streams it in 115 us this way against 126 us as
 // one-unit runs. The waves meet a barrier every two tiles, which keeps them
-// on the same blocks (C4 shape kernel 131 -> 127 us; every wave of the
+// on the same blocks (that shape's kernel 131 -> 127 us; every wave of the
 // workgroup walks the same tile counts); they share no LDS. Each writes its
 // own unit's normalised partial and log2-sum-exp per piece, to slot
 // ((b * NUG + ug) + w) * UW + i (NUG = units / UW groups per request).
