@@ -26,7 +26,10 @@ served in part from the MALL when steps run back to back, so by default
 (``--mall-flush auto``) a 512 MiB buffer is read before every timed sample
 of those (a read, so that no dirty lines are left to write back during the
 sample): outside the HIP-event brackets of the kernels, and its own
-event-timed duration is taken out of the step's wall time. Above that the
+event-timed duration is taken out of the eager steps' wall time. Their
+graph-timed step is a graph of the K steps, each behind the flush, less a
+graph of the K flushes alone, so that neither the flush nor a replay's
+start-up counts as step time. Above that the
 steps run back to back with no flush: the GQA decode shape over the FP8
 cache (414 MB of K/V) measured its attention kernel at 75.7-77.1 us back to
 back and 72.9-73.0 us with a flush before every step, so the MALL serves it
@@ -123,6 +126,30 @@ class MallFlush:
 
     def __call__(self) -> None:
         torch.sum(self.buf, dim=0, out=self.sink)
+
+
+class ProbeFlush:
+    """The same eviction as MallFlush, made with the library's read probe
+    (ikl_hbm_read_probe) over its own 512 MiB buffer: one kernel launch that
+    records nothing but itself into a HIP graph (torch's sum over many
+    blocks also records a memset node). Measured on the MQA 32/1 hd128 bf16
+    B64 x U[1024, 4096] step: 29.5 us median after it against 29.6 us after
+    MallFlush, so its streaming loads evict the MALL alike."""
+
+    def __init__(self, device: torch.device):
+        from inferkernellab_amd import _lib
+
+        self.lib = _lib.load()
+        self.check = _lib.check
+        self.buf = torch.ones((512 << 20) // 4, dtype=torch.int32, device=device)
+        self.sink = torch.zeros(1 << 14, dtype=torch.int32, device=device)
+        self.device = device
+
+    def __call__(self) -> None:
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        self.check(self.lib.ikl_hbm_read_probe(ctypes.c_void_p(self.buf.data_ptr()), self.buf.numel() * 4,
+                                               ctypes.c_void_p(self.sink.data_ptr()), self.sink.numel() * 4,
+                                               ctypes.c_void_p(stream)), "MALL flush (read probe)")
 
 
 def build_workload(name: str, device: torch.device, seed: int = 0, head_major: bool | None = None):
@@ -1042,20 +1069,29 @@ def measure_decode(workload: str, device: torch.device, *, steps: int, warmup: i
         # kernel. A model's decode graph holds one attention step per layer,
         # so that cost is shared by all of them: the K timed steps are
         # captured back to back in one graph and replayed once (exactly K
-        # steps). Workloads that flush the MALL before every step replay a
-        # one-step graph per step instead (the flush sits between replays).
+        # steps). Workloads that flush the MALL before every step capture
+        # the flush in front of each step of that graph, and a second graph
+        # of the K flushes alone; the step time is their difference over K.
         # The one-step-per-replay rate is reported beside it.
-        def capture(n: int) -> torch.cuda.CUDAGraph:
+        def capture(n: int, body=None) -> torch.cuda.CUDAGraph:
+            body = body or run_step
             side = torch.cuda.Stream(device)
             side.wait_stream(torch.cuda.current_stream(device))
             with torch.cuda.stream(side):
-                run_step()
+                body()
             torch.cuda.current_stream(device).wait_stream(side)
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 for _ in range(n):
-                    run_step()
+                    body()
             return g
+
+        def replay_s(g: torch.cuda.CUDAGraph) -> float:
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            g.replay()
+            torch.cuda.synchronize()
+            return time.perf_counter() - t
 
         one = capture(1)
         for _ in range(warmup):
@@ -1073,13 +1109,25 @@ def measure_decode(workload: str, device: torch.device, *, steps: int, warmup: i
         if flush_buf is None:
             many = capture(steps)
             many.replay()  # warm
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            many.replay()
-            torch.cuda.synchronize()
-            wall_s = time.perf_counter() - t0
+            wall_s = replay_s(many)
             step_mode = "hip graph of the K steps back to back, replayed once"
             del many
+        else:
+            probe = ProbeFlush(device)
+
+            def flushed_step() -> None:
+                probe()
+                run_step()
+
+            both, flushes = capture(steps, flushed_step), capture(steps, probe)
+            both.replay()  # warm
+            flushes.replay()
+            # median of 5 interleaved pairs of replays
+            diffs = sorted(replay_s(both) - replay_s(flushes) for _ in range(5))
+            wall_s = diffs[len(diffs) // 2]
+            step_mode = ("hip graph of the K steps, each behind a 512 MiB MALL flush read, minus a graph of the "
+                         "K flushes alone (median of 5 pairs of replays)")
+            del both, flushes, probe
         del one
     torch.cuda.synchronize()
     # every timed step recomputes the checked output (same inputs; the
@@ -1167,8 +1215,10 @@ def decode_record(m) -> dict:
         "ms_per_step": round(ms_per_step, 4),
         "us_per_step": round(ms_per_step * 1e3, 1),
         "step_mode": m["step_mode"],
-        "step_timing": ("wall clock around the K steps, synchronized on both sides, minus the "
-                        "event-timed 512 MiB MALL flush read before each step" if m["flush"]
+        "step_timing": (("wall clock around the graph of the K flushed steps minus that around the graph of "
+                         "the K flushes, each synchronized on both sides" if m["single_graph_us"] is not None
+                         else "wall clock around the K steps, synchronized on both sides, minus the "
+                              "event-timed 512 MiB MALL flush read before each step") if m["flush"]
                         else "wall clock around the K steps, synchronized on both sides"),
         "eager_us_per_step": round(m["eager_wall_s"] * 1e6 / k_steps, 1),
         "one_step_graph_us_per_step": (round(m["single_graph_us"], 1) if m["single_graph_us"] is not None
