@@ -67,6 +67,10 @@ WORKLOADS = {
     "mqa32x1_hd128_bf16_b64_ctx1k-4k": (64, 32, 1, 128, torch.bfloat16, 1024, 4096, None, 0.5, None),
     # the GQA decode shape over the FP8 (E4M3, per-row scale) cache format
     "gqa32x8_hd128_fp8kv_b32_ctx4k-8k": (32, 32, 8, 128, torch.bfloat16, 4096, 8192, 20000, 1.0, None, "fp8"),
+    # one GPU's share of that GQA 32/8 decode shape when its KV heads are split over 8 and 2 GPUs
+    # (same lengths and tables; each GPU attends its KV heads and their query heads)
+    "gqa4x1_hd128_bf16_b32_ctx4k-8k": (32, 4, 1, 128, torch.bfloat16, 4096, 8192, 20000, 1.0, None),
+    "gqa16x4_hd128_bf16_b32_ctx4k-8k": (32, 16, 4, 128, torch.bfloat16, 4096, 8192, 20000, 1.0, None),
     # the shapes the reference publishes its Triton kernel's A100 timings on (head_dim 64, block 16,
     # uniform contexts; docs/benchmark_report.md:45-52)
     "gqa32x8_hd64_fp16_b4_ctx512": (4, 32, 8, 64, torch.float16, 512, 512, None, 1.0, None),
@@ -1487,6 +1491,11 @@ DEFAULT_CONFIGS = (
      "GQA 32/8 hd128 bf16 B32 x U[4096, 8192] with split-context partitions of 512 tokens + reduce"),
     ("gqa_fp8kv", "gqa32x8_hd128_fp8kv_b32_ctx4k-8k", None,
      "the GQA decode configuration over the FP8 (E4M3, per-row scale) KV cache"),
+    ("gqa_kv_heads_over_8_gpus", "gqa4x1_hd128_bf16_b32_ctx4k-8k", None,
+     "one GPU's share of the GQA 32/8 hd128 bf16 B32 x U[4096, 8192] step when its KV heads are split over 8 "
+     "GPUs: 4 / 1 heads, the same lengths and tables"),
+    ("gqa_kv_heads_over_2_gpus", "gqa16x4_hd128_bf16_b32_ctx4k-8k", None,
+     "one GPU's share of the same step over 2 GPUs: 16 / 4 heads"),
 )
 
 
