@@ -251,6 +251,10 @@ MfmaShape mfma_launch_shape(bool balanced, int group_size, int unitw = 1);
 // once on the current device.
 int mfma_streamk_capacity(int dtype, int head_dim, int group_size, bool kv_fp8, int unitw = 1);
 
+// Workgroups of the fixed-partition MFMA kernel (units of `group_size`
+// heads) resident at once on the current device.
+int mfma_fixed_capacity(int dtype, int head_dim, int group_size, bool kv_fp8);
+
 // Units per workgroup the balanced split uses for `units` units of
 // `group_size` heads per request: the largest of 8, 4, 2 dividing `units`
 // for units of up to 16 heads, else 1 (one-unit runs).

@@ -753,9 +753,8 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl, bool fold_waves = tru
     return fail(IKL_EUNSUPPORTED, "partition_size -2 (the balanced split) needs the MFMA kernel family");
   const int64_t t_max = units * ((maxctx + 15) / 16);
   // 32-head units also take the balanced split as soon as their 512-token
-  // fixed partitions would not fit one round of resident workgroups (the
-  // balanced split's 2-wave runs hold the same resources as the fixed
-  // kernel's 2-wave workgroups). MQA 32/1 hd128 bf16, whole operation: B80 x
+  // fixed partitions would not fit one round of the fixed kernel's resident
+  // workgroups. MQA 32/1 hd128 bf16, whole operation: B80 x
   // U[1024, 4096] (640 workgroups for 512 resident) 46.6 -> 39.4 us, B48 x
   // U[4096, 8192] 53.2 -> 44.9, B128 54.6 -> 49.1; at or under one round
   // the fixed partitions stay faster (B64 x U[1024, 4096] 32.8 vs 35.3 us,
@@ -763,7 +762,7 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl, bool fold_waves = tru
   bool past_one_round = false;
   if (a->partition_size == 0 && pl.path == IKL_PATH_MFMA_GROUPED && pl.group_size > 16)
     past_one_round = units * ((maxctx + 511) / 512) >
-                     mfma_streamk_capacity(a->dtype, a->head_dim, pl.group_size, pl.kv_fp8);
+                     mfma_fixed_capacity(a->dtype, a->head_dim, pl.group_size, pl.kv_fp8);
   const bool want_balanced =
       a->partition_size == -2 ||
       (a->partition_size == 0 && pl.path == IKL_PATH_MFMA_GROUPED && (t_max > SK_MIN_BATCH_TILES || past_one_round));
@@ -827,7 +826,7 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl, bool fold_waves = tru
       // U[4096, 8192] 29.2 -> 26.8 us, B32 x U[1024, 4096] 28.7 -> 25.1, B64
       // x 2048 29.3 -> 27.0, B32 x 2048 22.6 -> 22.0; B64 x U[1024, 4096] keeps
       // 512.
-      const int64_t cap_wg = mfma_streamk_capacity(a->dtype, a->head_dim, pl.group_size, pl.kv_fp8);
+      const int64_t cap_wg = mfma_fixed_capacity(a->dtype, a->head_dim, pl.group_size, pl.kv_fp8);
       P = 128;
       while (P < 512 && units * ((maxctx + P - 1) / P) > cap_wg) P *= 2;
     }

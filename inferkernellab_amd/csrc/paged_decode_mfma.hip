@@ -267,9 +267,14 @@ struct WaveTiles {
     };
 
     // MASK: the tile has fewer than 16 valid rows (the run's last tile, or
-    // a masked block); full tiles skip the masking.
-    auto compute = [&](Tile &T, auto mask) {
-      constexpr bool MASK = decltype(mask)::value;
+    // a masked block). Full and partial tiles share this one body, the
+    // masks behind a wave-uniform branch: a body compiled per case (masks
+    // compiled out of full tiles) held the accumulators in two register
+    // sets, copied between them where the cases met (32-head units: 256
+    // VGPRs + 85 AGPRs of spills against 213 VGPRs; the GQA 32/8 decode
+    // kernel over the FP8 cache 73.9-76.5 -> 72.8-74.7 us).
+    auto compute = [&](Tile &T) {
+      const bool MASK = T.n_valid < TILE;
       wave_lds_sync();  // the previous tile's LDS reads come before these stores
       // stage V row-major in LDS (rows past the tile are never read)
 #pragma unroll
@@ -324,7 +329,7 @@ struct WaveTiles {
       if constexpr (KV8) {
         kscale = T.ks * p.scale_log2;
         vscale = T.vs;
-        if constexpr (MASK) {
+        if (MASK) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) vscale[i] = 4 * grp + i < T.n_valid ? vscale[i] : 0.f;
         }
@@ -334,9 +339,10 @@ struct WaveTiles {
       for (int g = 0; g < NG; ++g) {
         float sc[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sc[i] = sa[g][i] * kscale[i];
-          if constexpr (MASK) sc[i] = 4 * grp + i < T.n_valid ? sc[i] : -INFINITY;
+        for (int i = 0; i < 4; ++i) sc[i] = sa[g][i] * kscale[i];
+        if (MASK) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sc[i] = 4 * grp + i < T.n_valid ? sc[i] : -INFINITY;
         }
         float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
         tmax = max_xor32(max_xor16(tmax));
@@ -381,10 +387,7 @@ struct WaveTiles {
       }
     };
 
-    auto run = [&](Tile &T) {
-      if (T.n_valid == TILE) compute(T, std::false_type{});
-      else compute(T, std::true_type{});
-    };
+    auto run = [&](Tile &T) { compute(T); };
     // software pipeline: the next tile's loads fly while a tile computes (a
     // tile's registers taking the load two ahead right after it is staged
     // in LDS measured slower: GQA 32/8 hd128 bf16 B32 x U[4096, 8192]
@@ -458,7 +461,13 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
   // staged [NH heads x D] block, which the workgroup sums. The uses never
   // overlap.
   constexpr int SLOT = WT::ST_BYTES > WT::TILE_BYTES ? WT::ST_BYTES : WT::TILE_BYTES;
-  __shared__ __attribute__((aligned(16))) char lds[WAVES * SLOT];
+  // 32-head units of 96 or 128 dims ask for at least 56 KiB, so that a CU
+  // holds two of these 2-wave workgroups, one wave per SIMD: their
+  // registers would allow two waves per SIMD, and then the workgroups of a
+  // launch that fits one round pile up on fewer CUs (MQA 32/1 hd128 bf16
+  // B64 x U[1024, 4096], 347 workgroups: 25.5 -> 28.2 us).
+  constexpr int LDS_FLOOR = NG == 2 && D >= 96 ? 56 * 1024 : 0;
+  __shared__ __attribute__((aligned(16))) char lds[WAVES * SLOT > LDS_FLOOR ? WAVES * SLOT : LDS_FLOOR];
   __shared__ float lds_m[WAVES][NH], lds_l[WAVES][NH];
 
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -997,6 +1006,24 @@ int streamk_capacity_for(int unitw) {
   return resident_capacity(paged_decode_mfma_streamk_kernel<Tag, D, NG, SKW, KV8>, 64 * SKW, NG == 1 ? 8 : 4, c1);
 }
 
+// Resident workgroups of the fixed-partition kernel (its LDS included).
+template <typename Tag, int D, int NG, bool KV8>
+int fixed_capacity_for() {
+  constexpr int WAVES = wg_waves<NG>();
+  static std::atomic<int> c[64] = {};
+  return resident_capacity(paged_decode_mfma_kernel<Tag, D, NG, WAVES, KV8>, 64 * WAVES, NG == 1 ? 8 : 4, c);
+}
+
+template <typename Tag, int NG, bool KV8>
+int fixed_capacity_dim(int d) {
+  switch (d) {
+    case 32: return fixed_capacity_for<Tag, 32, NG, KV8>();
+    case 64: return fixed_capacity_for<Tag, 64, NG, KV8>();
+    case 96: return fixed_capacity_for<Tag, 96, NG, KV8>();
+    default: return fixed_capacity_for<Tag, 128, NG, KV8>();
+  }
+}
+
 template <typename Tag, int NG, bool KV8>
 int capacity_dim(int d, int unitw) {
   switch (d) {
@@ -1044,6 +1071,16 @@ int mfma_streamk_capacity(int dtype, int head_dim, int group_size, bool kv_fp8, 
   if (bf)
     return two ? capacity_kv<bf16_tag, 2>(head_dim, kv_fp8, 1) : capacity_kv<bf16_tag, 1>(head_dim, kv_fp8, unitw);
   return two ? capacity_kv<f16_tag, 2>(head_dim, kv_fp8, 1) : capacity_kv<f16_tag, 1>(head_dim, kv_fp8, unitw);
+}
+
+int mfma_fixed_capacity(int dtype, int head_dim, int group_size, bool kv_fp8) {
+  const bool two = group_size > 16;
+  if (dtype == IKL_BF16) {
+    if (two) return kv_fp8 ? fixed_capacity_dim<bf16_tag, 2, true>(head_dim) : fixed_capacity_dim<bf16_tag, 2, false>(head_dim);
+    return kv_fp8 ? fixed_capacity_dim<bf16_tag, 1, true>(head_dim) : fixed_capacity_dim<bf16_tag, 1, false>(head_dim);
+  }
+  if (two) return kv_fp8 ? fixed_capacity_dim<f16_tag, 2, true>(head_dim) : fixed_capacity_dim<f16_tag, 2, false>(head_dim);
+  return kv_fp8 ? fixed_capacity_dim<f16_tag, 1, true>(head_dim) : fixed_capacity_dim<f16_tag, 1, false>(head_dim);
 }
 
 int mfma_streamk_unitw(int64_t units, int group_size) {
