@@ -266,15 +266,15 @@ struct WaveTiles {
       for (int u = 0; u < VLOADS; ++u) T.v[u] = __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane[u], 0, CPOL_NT);
     };
 
-    // MASK: the tile has fewer than 16 valid rows (the run's last tile, or
-    // a masked block). Full and partial tiles share this one body, the
+    // partial: the tile has fewer than 16 valid rows (the run's last tile,
+    // or a masked block). Full and partial tiles share this one body, the
     // masks behind a wave-uniform branch: a body compiled per case (masks
     // compiled out of full tiles) held the accumulators in two register
     // sets, copied between them where the cases met (32-head units: 256
     // VGPRs + 85 AGPRs of spills against 213 VGPRs; the GQA 32/8 decode
     // kernel over the FP8 cache 73.9-76.5 -> 72.8-74.7 us).
     auto compute = [&](Tile &T) {
-      const bool MASK = T.n_valid < TILE;
+      const bool partial = T.n_valid < TILE;
       wave_lds_sync();  // the previous tile's LDS reads come before these stores
       // stage V row-major in LDS (rows past the tile are never read)
 #pragma unroll
@@ -329,7 +329,7 @@ struct WaveTiles {
       if constexpr (KV8) {
         kscale = T.ks * p.scale_log2;
         vscale = T.vs;
-        if (MASK) {
+        if (partial) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) vscale[i] = 4 * grp + i < T.n_valid ? vscale[i] : 0.f;
         }
@@ -340,7 +340,7 @@ struct WaveTiles {
         float sc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) sc[i] = sa[g][i] * kscale[i];
-        if (MASK) {
+        if (partial) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) sc[i] = 4 * grp + i < T.n_valid ? sc[i] : -INFINITY;
         }
@@ -962,10 +962,11 @@ void launch_kv(int d, const AttnParams &p, dim3 grid, hipStream_t s) {
   else launch_dim<Tag, NG, false>(d, p, grid, s);
 }
 
-// Resident workgroups of the balanced-split kernel on the current device
-// (CUs x workgroups per CU), cached per device; 256 CUs x the kernel's
-// waves per CU (8 for 16-head units, 4 for 32-head) / its waves per
-// workgroup when no device answers (planning on a host without a GPU).
+// Resident workgroups of a kernel on the current device (CUs x workgroups
+// per CU, its registers and LDS included), cached per device; 256 CUs x
+// the kernel's waves per CU (8 for 16-head units, 4 for 32-head) / its
+// waves per workgroup when no device answers (planning on a host without a
+// GPU).
 template <typename K>
 int resident_capacity(K kernel, int threads, int waves_per_cu, std::atomic<int> *cache) {
   constexpr int MAX_DEV = 64;
