@@ -255,6 +255,9 @@ int mfma_streamk_capacity(int dtype, int head_dim, int group_size, bool kv_fp8, 
 // heads) resident at once on the current device.
 int mfma_fixed_capacity(int dtype, int head_dim, int group_size, bool kv_fp8);
 
+// Compute units of the current device (256 when no device answers).
+int mfma_cu_count();
+
 // Units per workgroup the balanced split uses for `units` units of
 // `group_size` heads per request: the largest of 8, 4, 2 dividing `units`
 // for units of up to 16 heads, else 1 (one-unit runs).

@@ -818,17 +818,21 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl, bool fold_waves = tru
     P = 512;
     while (P > 128 && units * ((maxctx + P - 1) / P) < 160) P /= 2;
     if (pl.group_size > 16) {
-      // 32-head units: the shortest of 128, 256 and 512 tokens whose
-      // workgroups fit one round of resident workgroups (past 512 the
-      // balanced split runs instead). Sweeping MQA 32/1 hd128 bf16 over
-      // B4-B64 x {512, 2048, U[1024, 4096], U[4096, 8192]} (whole operation)
-      // this picked the fastest fixed size on 15 of 16 shapes: B16 x
-      // U[4096, 8192] 29.2 -> 26.8 us, B32 x U[1024, 4096] 28.7 -> 25.1, B64
-      // x 2048 29.3 -> 27.0, B32 x 2048 22.6 -> 22.0; B64 x U[1024, 4096] keeps
-      // 512.
+      // 32-head units: the longest of 128 ... 1024 tokens that still
+      // launches a workgroup per CU (two per CU over the FP8 cache, whose
+      // tiles carry half the bytes), and no more workgroups than are
+      // resident at once (past that at 512 tokens the balanced split runs
+      // instead). Sweeping MQA 32/1 over 128-2048 tokens (whole step, MALL
+      // flushed) this picked the fastest size, or one within 1 %, on all 8
+      // shapes: hd128 bf16 B64 x U[1024, 4096] (1024), B32 x U[4096, 8192]
+      // (1024), B16 x U[1024, 4096] (256), B64 x 2048 (512), B8 x 512 (128),
+      // the FP8 cache B64 x U[1024, 4096] (512), hd96 B64 x U[1024, 4096]
+      // (1024) and hd64 B16 x 2048 (128).
       const int64_t cap_wg = mfma_fixed_capacity(a->dtype, a->head_dim, pl.group_size, pl.kv_fp8);
+      const int64_t target = (int64_t)mfma_cu_count() * (pl.kv_fp8 ? 2 : 1);
       P = 128;
-      while (P < 512 && units * ((maxctx + P - 1) / P) > cap_wg) P *= 2;
+      while (P < 1024 && (units * ((maxctx + 2 * P - 1) / (2 * P)) >= target || units * ((maxctx + P - 1) / P) > cap_wg))
+        P *= 2;
     }
   } else {
     P = 512;

@@ -461,13 +461,7 @@ __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_m
   // staged [NH heads x D] block, which the workgroup sums. The uses never
   // overlap.
   constexpr int SLOT = WT::ST_BYTES > WT::TILE_BYTES ? WT::ST_BYTES : WT::TILE_BYTES;
-  // 32-head units of 96 or 128 dims ask for at least 56 KiB, so that a CU
-  // holds two of these 2-wave workgroups, one wave per SIMD: their
-  // registers would allow two waves per SIMD, and then the workgroups of a
-  // launch that fits one round pile up on fewer CUs (MQA 32/1 hd128 bf16
-  // B64 x U[1024, 4096], 347 workgroups: 25.5 -> 28.2 us).
-  constexpr int LDS_FLOOR = NG == 2 && D >= 96 ? 56 * 1024 : 0;
-  __shared__ __attribute__((aligned(16))) char lds[WAVES * SLOT > LDS_FLOOR ? WAVES * SLOT : LDS_FLOOR];
+  __shared__ __attribute__((aligned(16))) char lds[WAVES * SLOT];
   __shared__ float lds_m[WAVES][NH], lds_l[WAVES][NH];
 
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -903,11 +897,16 @@ __global__ __launch_bounds__(64 * UW) __attribute__((amdgpu_waves_per_eu(2, 8)))
   }
 }
 
-// Waves sharing one fixed partition: 4 for 16-head units; 2 for 32-head
-// units (their staged [32 x D] blocks would exceed 64 KB of LDS at 4).
+// Waves sharing one fixed partition: 4. For 32-head units that is 68 KB
+// of LDS at 128 dims (their staged [32 x D] blocks), two workgroups and
+// two waves per SIMD on a CU; with 2 waves per workgroup, one per SIMD,
+// each wave walked twice the tiles (MQA 32/1 hd128 bf16 step, planned as
+// below: B64 x U[1024, 4096] 27.4 -> 26.3 us, B16 x U[1024, 4096] 16.5 ->
+// 14.6, B64 x 2048 23.9 -> 21.3, over the FP8 cache B64 x U[1024, 4096]
+// 26.9 -> 22.7).
 template <int NG>
 constexpr int wg_waves() {
-  return NG == 1 ? 4 : 2;
+  return 4;
 }
 
 // Waves per balanced-split workgroup. 32-head units take 2: their pieces'
@@ -1007,12 +1006,13 @@ int streamk_capacity_for(int unitw) {
   return resident_capacity(paged_decode_mfma_streamk_kernel<Tag, D, NG, SKW, KV8>, 64 * SKW, NG == 1 ? 8 : 4, c1);
 }
 
-// Resident workgroups of the fixed-partition kernel (its LDS included).
+// Resident workgroups of the fixed-partition kernel (its LDS included;
+// without a device, two waves per SIMD).
 template <typename Tag, int D, int NG, bool KV8>
 int fixed_capacity_for() {
   constexpr int WAVES = wg_waves<NG>();
   static std::atomic<int> c[64] = {};
-  return resident_capacity(paged_decode_mfma_kernel<Tag, D, NG, WAVES, KV8>, 64 * WAVES, NG == 1 ? 8 : 4, c);
+  return resident_capacity(paged_decode_mfma_kernel<Tag, D, NG, WAVES, KV8>, 64 * WAVES, 8, c);
 }
 
 template <typename Tag, int NG, bool KV8>
@@ -1082,6 +1082,25 @@ int mfma_fixed_capacity(int dtype, int head_dim, int group_size, bool kv_fp8) {
   }
   if (two) return kv_fp8 ? fixed_capacity_dim<f16_tag, 2, true>(head_dim) : fixed_capacity_dim<f16_tag, 2, false>(head_dim);
   return kv_fp8 ? fixed_capacity_dim<f16_tag, 1, true>(head_dim) : fixed_capacity_dim<f16_tag, 1, false>(head_dim);
+}
+
+int mfma_cu_count() {
+  constexpr int MAX_DEV = 64;
+  static std::atomic<int> cache[MAX_DEV] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  const int known = cache[dev].load(std::memory_order_acquire);
+  if (known > 0) return known;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  cache[dev].store(cus, std::memory_order_release);
+  return cus;
 }
 
 int mfma_streamk_unitw(int64_t units, int group_size) {

@@ -136,7 +136,7 @@ def test_split_choice_by_batch_size_on_the_mfma_family():
     a = _args(partition_size=0, max_context_len=512)
     assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 0
     # 32-head units: balanced once 512-token partitions exceed one round of
-    # resident workgroups (512 without a device: 256 CUs x 2 two-wave groups)
+    # resident workgroups (512 without a device: 256 CUs x 2 four-wave groups)
     if not torch.cuda.is_available():
         a = _args(partition_size=0, max_context_len=4096, batch=64, num_kv_heads=1)  # 512 workgroups
         assert ops.launch_config(a)["split"] == "fixed_partitions"
@@ -144,6 +144,13 @@ def test_split_choice_by_batch_size_on_the_mfma_family():
         assert ops.launch_config(a)["split"] == "balanced"
         a = _args(partition_size=0, max_context_len=2048, batch=96, num_kv_heads=1)  # 384
         assert ops.launch_config(a)["split"] == "fixed_partitions"
+        # their fixed partitions: the longest of 128-1024 tokens that still
+        # launches a workgroup per CU (two over the FP8 cache)
+        for batch, ctx, want in ((64, 4096, 1024), (16, 4096, 256), (64, 2048, 512), (8, 512, 128)):
+            a = _args(partition_size=0, max_context_len=ctx, batch=batch, num_kv_heads=1)
+            assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == want, (batch, ctx)
+            cfg = ops.launch_config(a)
+            assert (cfg["split"], cfg["num_warps"]) == ("fixed_partitions", 4)
     # -2: the balanced split on a small batch too
     a = _args(partition_size=-2, max_context_len=1024, batch=2)
     part = lib.ikl_paged_attention_partition_size(ctypes.byref(a))
