@@ -909,16 +909,18 @@ constexpr int wg_waves() {
   return 4;
 }
 
-// Waves per balanced-split workgroup. 32-head units take 2: their pieces'
-// partials are 16 KB each, and merging two waves' shares in LDS halves them
-// (MQA 32/1 hd128 bf16, kernel: B64 x U[1024, 4096] 28.8 -> 27.5 us, B128
-// 41.8 -> 40.3, B32 x U[4096, 8192] 31.0 -> 29.6). 16-head units keep one
-// wave per run: with 4 waves sharing each piece a wave meets more piece
-// starts and barriers, and the GQA 32/8 bf16 B32 x U[4096, 8192] kernel
-// went from 137.7 to 144.1 us.
+// Waves per balanced-split workgroup. 32-head units take 4: their pieces'
+// partials are 16 KB each, and merging the waves' shares in LDS divides
+// them (MQA 32/1 hd128 bf16, kernel: B64 x U[1024, 4096] 28.8 -> 27.5 us
+// from 1 to 2 waves, B128 41.8 -> 40.3, B32 x U[4096, 8192] 31.0 -> 29.6;
+// whole step from 2 to 4 waves: B128 x U[1024, 4096] 43.9-44.6 -> 42.1-42.2
+// us, B48 x U[4096, 8192] 38.1-38.2 -> 36.3-36.7, over the FP8 cache
+// unchanged). 16-head units keep one wave per run: with 4 waves sharing
+// each piece a wave meets more piece starts and barriers, and the GQA 32/8
+// bf16 B32 x U[4096, 8192] kernel went from 137.7 to 144.1 us.
 template <int NG>
 constexpr int sk_wg_waves() {
-  return NG == 1 ? 1 : 2;
+  return NG == 1 ? 1 : 4;
 }
 
 template <typename Tag, int D, int NG, bool KV8>

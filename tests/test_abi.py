@@ -158,12 +158,12 @@ def test_split_choice_by_batch_size_on_the_mfma_family():
     # 1024 tiles at the longest context, the 8 units of a request in one
     # workgroup: 128 (request, tile) entries, at least 4 per run: 32 runs of 4
     assert part == 64 and ops.launch_config(a)["workgroups"] == 32
-    # 32-head units run 2-wave workgroups, at least 4 tiles per wave
+    # 32-head units run 4-wave workgroups, at least 4 tiles per wave
     a = _args(partition_size=-2, max_context_len=4096, batch=64, num_kv_heads=1)
     cfg = ops.launch_config(a)
-    assert (cfg["split"], cfg["num_warps"]) == ("balanced", 2)
-    if not torch.cuda.is_available():  # 256 CUs x 2 workgroups of 2 waves
-        assert cfg["workgroups"] == 512
+    assert (cfg["split"], cfg["num_warps"]) == ("balanced", 4)
+    if not torch.cuda.is_available():  # 256 CUs x 1 workgroup of 4 waves
+        assert cfg["workgroups"] == 256
     # -2 where the MFMA family does not run (fp32) is refused
     a = _args(partition_size=-2, max_context_len=1024, dtype=_lib.IKL_F32)
     assert lib.ikl_paged_attention_workspace_size(ctypes.byref(a)) == _lib.IKL_EUNSUPPORTED

@@ -195,7 +195,7 @@ def test_repeat_runs_are_bit_identical():
 # batches above 32768 tiles): the batch's tiles are cut into one equal run
 # per workgroup (for units of up to 16 heads, groups of 2, 4 or 8 units of a
 # request as the waves of one workgroup walking the same request tiles, or
-# one-wave runs when the units per request are odd; 2 waves for 32-head
+# one-wave runs when the units per request are odd; 4 waves for 32-head
 # units, which share each piece of the run and merge it in LDS), and the
 # pieces are merged per unit by the reduce.
 
@@ -247,7 +247,7 @@ def test_balanced_split_one_unit_across_many_waves():
 @pytest.mark.parametrize("heads,kv,dim,dtype", [(32, 1, 128, "float16"), (32, 1, 128, "bfloat16"),
                                                 (48, 2, 64, "bfloat16"), (40, 2, 96, "float16")])
 def test_balanced_split_32_head_units(heads, kv, dim, dtype):
-    """Units of 17-32 heads (MQA 32/1, and 24- and 20-head units) run 2-wave
+    """Units of 17-32 heads (MQA 32/1, and 24- and 20-head units) run 4-wave
     workgroups; ragged lengths (one token, one tile, a tile and one token,
     long) give pieces shorter than a workgroup's waves and pieces spanning
     several runs."""
@@ -260,12 +260,12 @@ def test_balanced_split_32_head_units(heads, kv, dim, dtype):
                      lengths=lengths, dtype=dtype, seed=45, kv_scale=0.5)
     _check(case, "paged_decode_attention_hip", label="sk-32head", partition_size=-2)
     cfg = ops.paged_decode_grouped_dot_autotune_config()
-    assert cfg["num_warps"] == 2
+    assert cfg["num_warps"] == 4
 
 
 @pytest.mark.parametrize("batch,lo,hi", [(1, 20000, 20000), (300, 1, 50)])
 def test_balanced_split_32_head_units_extremes(batch, lo, hi):
-    """2-wave runs of 32-head units: one MQA request of 20000 tokens split
+    """4-wave runs of 32-head units: one MQA request of 20000 tokens split
     over every run, and 300 short requests (the in-kernel request scan walks
     five 64-request chunks; many runs hold several whole requests)."""
     lengths = [int(x) for x in np.random.default_rng(46).integers(lo, hi + 1, size=batch)]
