@@ -1193,9 +1193,8 @@ def split_name(m) -> str:
         return "balanced (equal tile runs per resident workgroup)"
     if attn.launch["split"] != "none":
         return f"fixed partitions of {attn.partition_size} tokens"
-    if step.fused:
-        return ("attention alone: unsplit, up to 4 partitions per request folded into one multi-wave "
-                "workgroup; the step keeps them split for the reduce to carry the append")
+    if attn.launch["path"] != "mfma_grouped" and attn.launch["num_warps"] > 1:
+        return "none: up to 4 partitions per request folded into one multi-wave workgroup"
     return "none"
 
 
@@ -1246,9 +1245,10 @@ def decode_record(m) -> dict:
             "kv_block_layout": "[kv_heads, block_size, D]" if m["head_major"] else "[block_size, kv_heads, D]",
             "partition_size": attn.partition_size,
             "split": split_name(m),
-            "step": ("paged attention (split kernel + reduce) then 1-token KV append per request: "
-                     + ("two operator launches" if m["separate_append"] or not step.fused
-                        else "one library call, the append carried by the reduce kernel")),
+            "step": ("paged attention then a 1-token KV append per request: "
+                     + ("two operator launches" if m["separate_append"]
+                        else "one library call, the append carried by the reduce kernel" if step.fused
+                        else "one library call, the attention then the append kernel")),
             "kernels": ([n for n in attn.kernel_names() if n] + ["append_kv_kernel"] if m["separate_append"]
                         else list(step.kernel_names())),
             "parallelism": "single GPU",

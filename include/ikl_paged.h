@@ -352,15 +352,11 @@ int ikl_paged_decode_step(const ikl_paged_attention_args *attention, const ikl_a
 int32_t ikl_paged_decode_step_fused(const ikl_paged_attention_args *attention,
                                     const ikl_append_args *append);
 
-/* Workspace bytes that ikl_paged_decode_step may use with these arguments:
- * at least ikl_paged_attention_workspace_size. When the attention alone
- * would run unsplit with a request's partitions folded into one multi-wave
- * workgroup (the automatic split of the VALU family), the step keeps the
- * split instead if the append can ride on the reduce and the workspace
- * holds this many bytes, saving the append's own launch; with a smaller
- * workspace it runs the folded kernel and then the append. Negative on
- * invalid arguments. Planning only. No counterpart in the reference (see
- * ikl_paged_decode_step). */
+/* Workspace bytes that ikl_paged_decode_step uses with these arguments:
+ * the attention's (ikl_paged_attention_workspace_size); an unsplit
+ * attention, folded multi-wave workgroups included, is followed by the
+ * append's own launch. Negative on invalid arguments. Planning only. No
+ * counterpart in the reference (see ikl_paged_decode_step). */
 int64_t ikl_paged_decode_step_workspace_size(const ikl_paged_attention_args *attention,
                                              const ikl_append_args *append);
 

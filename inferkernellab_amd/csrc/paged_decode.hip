@@ -1129,16 +1129,13 @@ int run_attention(const ikl_paged_attention_args *a, const Plan &pl, const Fused
 
 // Whether a decode step's append rides on the reduce kernel (1), runs as
 // its own launch after the attention (0), or the arguments are invalid (<0).
-// The decode step's plan. When the attention alone would fold a request's
-// partitions into one unsplit VALU workgroup, the step keeps them split if
-// the append can ride on the reduce and the workspace holds the split's
-// partials (ikl_paged_decode_step_workspace_size reports that size): one
-// launch less than the folded kernel followed by the append (MHA fp16
-// B16 x 512: 24.7 + 4.0 us -> 24.0 + 4.0 us by kernel trace, the append
-// costing nothing on the reduce). `alt_ws` receives the split's workspace
-// size, or 0 when no alternative applies.
-int step_plan(const ikl_paged_attention_args *a, const ikl_append_args *app, Plan &pl, FusedAppend &f,
-              int64_t *alt_ws = nullptr) {
+// A split launch's reduce carries the append. An unsplit one (a VALU plan
+// folded into multi-wave workgroups included) is followed by the append
+// kernel: keeping such a plan split so that its reduce could carry the
+// append measured slower per step (MHA fp16 hd128 B16 x 512 27.8-28.6 ->
+// 26.8-27.3 us with the append kernel, B32 x 1024 88.4 -> 85.3, hd64 B16 x
+// 512 18.7-19.2 -> 16.9-17.1; fp32 GQA 32/8 hd64 B4 x 512 equal).
+int step_plan(const ikl_paged_attention_args *a, const ikl_append_args *app, Plan &pl, FusedAppend &f) {
   int rc = make_plan(a, pl);
   if (rc != IKL_OK) return rc;
   rc = prepare_fused_append(app, f);
@@ -1146,14 +1143,6 @@ int step_plan(const ikl_paged_attention_args *a, const ikl_append_args *app, Pla
   // an FP8 append rides along when its rows are in the query dtype (the
   // reduce kernel's element type)
   const bool can_fuse = rc == IKL_OK && f.rows > 0 && (!f.fp8 || f.src_dtype == a->dtype);
-  if (alt_ws) *alt_ws = 0;
-  if (can_fuse && !pl.split && pl.scalar_waves > 1) {
-    Plan alt;
-    if (make_plan(a, alt, false) == IKL_OK && alt.split) {
-      if (alt_ws) *alt_ws = alt.ws_bytes;
-      if (a->workspace && a->workspace_bytes >= alt.ws_bytes && aligned16(a->workspace)) pl = alt;
-    }
-  }
   return can_fuse && pl.split ? 1 : 0;
 }
 }  // namespace
@@ -1230,10 +1219,9 @@ extern "C" int64_t ikl_paged_decode_step_workspace_size(const ikl_paged_attentio
                                                         const ikl_append_args *app) {
   Plan pl;
   FusedAppend f;
-  int64_t alt = 0;
-  const int mode = step_plan(a, app, pl, f, &alt);
+  const int mode = step_plan(a, app, pl, f);
   if (mode < 0) return mode;
-  return std::max<int64_t>(pl.ws_bytes, alt);
+  return pl.ws_bytes;
 }
 
 extern "C" int32_t ikl_paged_decode_step_fused(const ikl_paged_attention_args *a, const ikl_append_args *app) {

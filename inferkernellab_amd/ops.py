@@ -696,12 +696,12 @@ class PreparedDecodeStep:
     (decode.py:480-487), enqueued by one library call
     (``ikl_paged_decode_step``). When the attention splits, the reduce
     kernel also carries the append — one launch less per step — with the
-    same result as calling the two separately (``fused`` tells which).
-    Where the attention alone would run unsplit on folded multi-wave
-    workgroups, the step keeps the split so that the reduce carries the
-    append; it then runs on its own copy of the attention's arguments with
-    a workspace of the step's size (``ikl_paged_decode_step_workspace_size``),
-    leaving ``attention`` and anything captured from it untouched."""
+    same result as calling the two separately (``fused`` tells which); an
+    unsplit attention is followed by the append's own launch. Should the
+    step need more workspace than the attention holds
+    (``ikl_paged_decode_step_workspace_size``), it runs on its own copy of
+    the attention's arguments with a workspace of that size, leaving
+    ``attention`` and anything captured from it untouched."""
 
     def __init__(self, attention: PreparedPagedAttention, append: PreparedAppend):
         if attention.device != append.device:

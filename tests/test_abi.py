@@ -516,11 +516,12 @@ def test_decode_step_fuses_the_append_into_the_reduce(attn_kw, append_kw, expect
     assert lib.ikl_paged_decode_step_fused(ctypes.byref(a), ctypes.byref(_append_args(**append_kw))) == expect
 
 
-def test_decode_step_keeps_the_split_that_carries_the_append():
-    """MHA fp16 B16 x 512 on the VALU family: the attention alone folds each
+def test_decode_step_on_a_folded_plan_appends_with_its_own_launch():
+    """MHA fp16 B16 x 512 on the VALU family: the attention folds each
     request's two partitions into one 2-wave workgroup and needs no
-    workspace; the step keeps the split (the reduce then carries the
-    append) when its workspace holds the split's partials."""
+    workspace; the step runs it and then the append kernel, whatever
+    workspace it is given (keeping the split for the reduce to carry the
+    append measured slower)."""
     lib = _lib.load()
     a = _args(dtype=_lib.IKL_F16, batch=16, num_heads=32, num_kv_heads=32, max_context_len=512)
     cfg = ops.launch_config(a)
@@ -528,20 +529,16 @@ def test_decode_step_keeps_the_split_that_carries_the_append():
     assert lib.ikl_paged_attention_workspace_size(ctypes.byref(a)) == 0
     app = _append_args(dtype=_lib.IKL_F16, num_kv_heads=32, num_tokens=16, key_stride_t=32 * 128,
                        value_stride_t=32 * 128)
-    need = lib.ikl_paged_decode_step_workspace_size(ctypes.byref(a), ctypes.byref(app))
-    rows = 16 * 2 * 32  # requests x 256-token partitions x heads
-    assert need >= rows * 128 * 4 + rows * 4
-    assert lib.ikl_paged_decode_step_fused(ctypes.byref(a), ctypes.byref(app)) == 0  # no workspace: folded
-    a.workspace, a.workspace_bytes = 0x100000, need - 16
-    assert lib.ikl_paged_decode_step_fused(ctypes.byref(a), ctypes.byref(app)) == 0  # too small
-    a.workspace_bytes = need
-    assert lib.ikl_paged_decode_step_fused(ctypes.byref(a), ctypes.byref(app)) == 1
-    a.workspace = 0x100008
-    assert lib.ikl_paged_decode_step_fused(ctypes.byref(a), ctypes.byref(app)) == 0  # not 16-byte aligned
-    # no alternative where the attention already splits, or with nothing to append
+    assert lib.ikl_paged_decode_step_workspace_size(ctypes.byref(a), ctypes.byref(app)) == 0
+    assert lib.ikl_paged_decode_step_fused(ctypes.byref(a), ctypes.byref(app)) == 0
+    a.workspace, a.workspace_bytes = 0x100000, 1 << 20
+    assert lib.ikl_paged_decode_step_fused(ctypes.byref(a), ctypes.byref(app)) == 0
+    # a split attention: the step's workspace is the attention's, and the reduce carries the append
     b = _args(max_context_len=8192)
-    assert lib.ikl_paged_decode_step_workspace_size(ctypes.byref(b), ctypes.byref(_append_args())) == \
-        lib.ikl_paged_attention_workspace_size(ctypes.byref(b))
+    need = lib.ikl_paged_attention_workspace_size(ctypes.byref(b))
+    assert need > 0 and lib.ikl_paged_decode_step_workspace_size(ctypes.byref(b), ctypes.byref(_append_args())) == need
+    b.workspace, b.workspace_bytes = 0x100000, need
+    assert lib.ikl_paged_decode_step_fused(ctypes.byref(b), ctypes.byref(_append_args())) == 1
     a.workspace, a.workspace_bytes = 0, 0
     assert lib.ikl_paged_decode_step_workspace_size(ctypes.byref(a), ctypes.byref(_append_args(num_tokens=0))) == 0
     assert lib.ikl_paged_decode_step_workspace_size(ctypes.byref(a), ctypes.byref(_append_args(key=0))) == \

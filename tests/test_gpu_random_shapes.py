@@ -4,7 +4,7 @@ groups), head_dim 16-128, fp16/bf16/fp32, block sizes 8/16/32, ragged
 batches of 1-70 requests up to 3000 tokens, and every split choice (the
 automatic one, unsplit, the balanced split and fixed partitions of
 64-512 tokens) through both entry points. This crosses the kernel families'
-planning rules (folded VALU workgroups, one-round MQA partitions, 2-wave
+planning rules (folded VALU workgroups, one-round MQA partitions, 4-wave
 balanced runs, the small-MHA routing) with shapes no dedicated test picks;
 40 more go over the FP8 cache. Bound: max-abs 2e-3 fp16, 1e-2 bf16, 1e-4 fp32, plus half an output ulp."""
 

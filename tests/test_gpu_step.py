@@ -80,36 +80,33 @@ def test_step_equals_attention_then_append(shape):
     assert step.kernel_names()[-1] == ("paged_decode_reduce_kernel" if fused else "append_kv_kernel")
 
 
-def test_step_keeps_the_split_where_the_attention_alone_folds():
-    """fp32 GQA 32/8 hd64, B4 x <= 512: the attention alone runs each
-    request's four 128-token partitions as one 4-wave workgroup (no split);
-    the step keeps them split so that the reduce carries the append. Its
-    output equals the attention over 128-token partitions bit for bit."""
+def test_step_over_a_folded_plan_appends_with_its_own_launch():
+    """fp32 GQA 32/8 hd64, B4 x <= 512: the attention runs each request's
+    four 128-token partitions as one 4-wave workgroup (no split, no
+    workspace); the step runs that kernel and then the append kernel. Its
+    output equals the attention alone bit for bit, and the cache equals
+    the separate append's."""
     from inferkernellab_amd import ops
 
     print("decode step over a folded VALU plan: B=4 H=32 Hkv=8 D=64 float32", flush=True)
     case, key, value, slots = _step_case(batch=4, heads=32, kv=8, head_dim=64, lengths=[512, 1, 300, 129],
                                          dtype="float32", seed=90)
-    fused_cache, ref_cache = case.device_cache(), case.device_cache()
+    step_cache, ref_cache = case.device_cache(), case.device_cache()
     q, tables, lens = case.device_query(), case.device_tables(), case.device_lengths()
-    attn = ops.PreparedPagedAttention(q, fused_cache, tables, lens, max_context_len=512)
+    attn = ops.PreparedPagedAttention(q, step_cache, tables, lens, max_context_len=512)
     assert (attn.launch["split"], attn.launch["num_warps"]) == ("none", 4)
     assert attn.workspace.numel() == 1  # the attention alone needs none
-    step = ops.PreparedDecodeStep(attn, ops.PreparedAppend(key, value, fused_cache, slots))
-    assert step.fused
-    assert step.kernel_names() == ("paged_decode_scalar_kernel", "paged_decode_reduce_kernel")
+    step = ops.PreparedDecodeStep(attn, ops.PreparedAppend(key, value, step_cache, slots))
+    assert not step.fused and step.workspace is None
+    assert step.kernel_names() == ("paged_decode_scalar_kernel", "append_kv_kernel")
     out = step().clone()
-    ref = ops.paged_decode_attention_hip(q, ref_cache, tables, lens, partition_size=128, max_context_len=512)
+    ref = ops.paged_decode_attention_hip(q, ref_cache, tables, lens, max_context_len=512)
     ops.append_kv_hip(key, value, ref_cache, slots)
-    assert attn._args.workspace_bytes == 0 and step.workspace is not None  # the step has its own copy
-    alone = attn().clone()  # still folded, without a workspace
     torch.cuda.synchronize()
     assert torch.equal(_bits(out), _bits(ref))
-    assert torch.equal(_bits(fused_cache.k), _bits(ref_cache.k))
-    assert torch.equal(_bits(fused_cache.v), _bits(ref_cache.v))
-    expected = case.expected()
-    assert max_abs_err(out, expected) <= ATOL["float32"]
-    assert max_abs_err(alone, expected) <= ATOL["float32"]
+    assert torch.equal(_bits(step_cache.k), _bits(ref_cache.k))
+    assert torch.equal(_bits(step_cache.v), _bits(ref_cache.v))
+    assert max_abs_err(out, case.expected()) <= ATOL["float32"]
 
 
 def test_step_appends_more_rows_than_one_pass_covers():
@@ -216,8 +213,7 @@ def test_step_on_random_shapes():
     """30 seeded random decode steps (dtype, heads, head_dim, batch, lengths,
     split choice): the step's output equals the oracle, and its cache equals
     a following ikl_append_kv bit for bit, whether the append rides on the
-    reduce or runs on its own (and where the step keeps a split that the
-    attention alone would fold)."""
+    reduce or runs on its own (folded attention plans included)."""
     import random
 
     from inferkernellab_amd import ops
