@@ -817,6 +817,17 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl, bool fold_waves = tru
     // B4 x 512 (11.9 -> 10.6 us) and MQA hd64 B16 x 2048 (16.4 -> 13.9 us)
     P = 512;
     while (P > 128 && units * ((maxctx + P - 1) / P) < 160) P /= 2;
+    if (pl.group_size <= 16 && units >= mfma_cu_count()) {
+      // A workgroup per CU without splitting (here at most 32768 tiles, so
+      // contexts of at most 2048 tokens): each (request, unit) runs unsplit
+      // on its workgroup's 4 waves, with no partials and no reduce. GQA
+      // 32/8 hd128 bf16 step (MALL flushed): B32 x 1024 28.2-28.4 -> 25.5-25.7
+      // us, B32 x 2048 49.2 -> 45.3, B32 x U[512, 1024] 24.8-25.3 ->
+      // 22.3-22.8, hd64 fp16 B32 x 1024 18.7-19.3 -> 15.2-15.4; with fewer
+      // units than CUs the split stays faster (B16 x 1024 17.2-17.7 against
+      // 18.8-19.0), and 384 units came out even (B48 x 1024 38.7 / 39.2).
+      P = maxctx;
+    }
     if (pl.group_size > 16) {
       // 32-head units: the longest of 128 ... 1024 tokens that still
       // launches a workgroup per CU (two per CU over the FP8 cache, whose

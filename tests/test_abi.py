@@ -123,8 +123,12 @@ def test_split_choice_by_batch_size_on_the_mfma_family():
     # B32 x 8 kv heads x 8192 tokens: 131072 tiles -> balanced (partition = a wave's run)
     a = _args(partition_size=0, max_context_len=8192)
     assert ops.launch_config(a)["split"] == "balanced"
-    # B32 x 8 x 1024: 16384 tiles -> fixed 512-token partitions (512 workgroups)
+    # B32 x 8 x 1024: 16384 tiles, 256 units (a workgroup per CU of 256) -> unsplit
     a = _args(partition_size=0, max_context_len=1024)
+    assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 0
+    assert ops.launch_config(a)["split"] == "none"
+    # B16 x 8 x 1024: 128 units -> fixed 512-token partitions (256 workgroups)
+    a = _args(partition_size=0, max_context_len=1024, batch=16)
     assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == 512
     # B2 x 8 x 1024: 16 units -> 32, 64, then 128 workgroups -> 128-token partitions
     a = _args(partition_size=0, max_context_len=1024, batch=2)
