@@ -697,11 +697,9 @@ class PreparedDecodeStep:
     (``ikl_paged_decode_step``). When the attention splits, the reduce
     kernel also carries the append — one launch less per step — with the
     same result as calling the two separately (``fused`` tells which); an
-    unsplit attention is followed by the append's own launch. Should the
-    step need more workspace than the attention holds
-    (``ikl_paged_decode_step_workspace_size``), it runs on its own copy of
-    the attention's arguments with a workspace of that size, leaving
-    ``attention`` and anything captured from it untouched."""
+    unsplit attention is followed by the append's own launch. The step
+    runs on the attention's own arguments and workspace
+    (``ikl_paged_decode_step_workspace_size`` equals the attention's)."""
 
     def __init__(self, attention: PreparedPagedAttention, append: PreparedAppend):
         if attention.device != append.device:
@@ -709,15 +707,12 @@ class PreparedDecodeStep:
         self._lib = _require_backend()
         self.attention, self.append = attention, append
         self._args = attention._args
-        self.workspace = None
         app = ctypes.byref(append._args)
         need = self._lib.ikl_paged_decode_step_workspace_size(ctypes.byref(self._args), app)
         _lib.check(need if need < 0 else 0, "decode step")
         if need > attention._args.workspace_bytes:
-            self._args = type(attention._args).from_buffer_copy(attention._args)
-            self.workspace = torch.empty(need, dtype=torch.uint8, device=attention.device)
-            self._args.workspace = self.workspace.data_ptr()
-            self._args.workspace_bytes = need
+            raise RuntimeError(f"decode step: needs {need} bytes of workspace, the attention holds "
+                               f"{attention._args.workspace_bytes}")
         mode = self._lib.ikl_paged_decode_step_fused(ctypes.byref(self._args), app)
         _lib.check(mode if mode < 0 else 0, "decode step")
         self.fused = mode == 1

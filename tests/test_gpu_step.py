@@ -97,7 +97,7 @@ def test_step_over_a_folded_plan_appends_with_its_own_launch():
     assert (attn.launch["split"], attn.launch["num_warps"]) == ("none", 4)
     assert attn.workspace.numel() == 1  # the attention alone needs none
     step = ops.PreparedDecodeStep(attn, ops.PreparedAppend(key, value, step_cache, slots))
-    assert not step.fused and step.workspace is None
+    assert not step.fused
     assert step.kernel_names() == ("paged_decode_scalar_kernel", "append_kv_kernel")
     out = step().clone()
     ref = ops.paged_decode_attention_hip(q, ref_cache, tables, lens, max_context_len=512)
