@@ -100,6 +100,7 @@ struct AttnParams {
   // entries, tile t at entry sk_seg_cost + t.
   int32_t sk_seg_cost;
   int32_t grid_spread;     // fixed-partition MFMA grid is request-fastest (spread_grid)
+  int32_t fixed_waves;     // waves per fixed-partition MFMA workgroup (4, or 8 for 32-head units over FP8)
   int64_t batch;
   int64_t cap_tokens;      // table_width * block_size: positions a table can map
   // FP8 KV cache (MFMA family): E4M3 codes with one fp32 scale per (token,
@@ -244,7 +245,8 @@ hipError_t launch_mfma_attention(int dtype, int head_dim, const AttnParams &p, d
 struct MfmaShape {
   int tile_tokens, waves_per_workgroup, stages;
 };
-MfmaShape mfma_launch_shape(bool balanced, int group_size, int unitw = 1);
+// fixed_waves: the plan's waves per fixed-partition workgroup (0: the default).
+MfmaShape mfma_launch_shape(bool balanced, int group_size, int unitw = 1, int fixed_waves = 0);
 
 // Workgroups of the balanced-split MFMA kernel (for units of `group_size`
 // heads; `unitw` units per workgroup for the unit-parallel form) resident at
@@ -254,6 +256,10 @@ int mfma_streamk_capacity(int dtype, int head_dim, int group_size, bool kv_fp8, 
 // Workgroups of the fixed-partition MFMA kernel (units of `group_size`
 // heads) resident at once on the current device.
 int mfma_fixed_capacity(int dtype, int head_dim, int group_size, bool kv_fp8);
+
+// Workgroups of its 8-wave form for 32-head units over the FP8 cache
+// resident at once on the current device.
+int mfma_fixed8_capacity(int dtype, int head_dim);
 
 // Compute units of the current device (256 when no device answers).
 int mfma_cu_count();

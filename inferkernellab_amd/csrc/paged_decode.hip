@@ -612,6 +612,7 @@ struct Plan {
   int64_t ws_bytes = 0;
   bool kv_fp8 = false;  // E4M3 cache with per-row scales (MFMA family only)
   int scalar_waves = 1;  // waves per workgroup of the VALU family (1, 2 or 4)
+  int fixed_waves = 4;   // waves per fixed-partition MFMA workgroup (8: 32-head units over the FP8 cache)
 };
 
 int elem_bytes(int dtype) {
@@ -844,6 +845,23 @@ int make_plan(const ikl_paged_attention_args *a, Plan &pl, bool fold_waves = tru
       P = 128;
       while (P < 1024 && (units * ((maxctx + 2 * P - 1) / (2 * P)) >= target || units * ((maxctx + P - 1) / P) > cap_wg))
         P *= 2;
+      // Over the FP8 cache, 1024-token partitions that give a workgroup per
+      // CU, all resident at once, run as 8-wave workgroups (two waves per
+      // SIMD, 8 tiles each) in place of 512-token partitions at two 4-wave
+      // workgroups per CU. MQA 32/1 hd128 over the FP8 cache, whole step,
+      // MALL flushed: B64 x U[1024, 4096] 22.8-22.9 -> 21.5-21.6 us, B32 x
+      // U[4096, 8192] 23.9-24.2 -> 21.2-21.8; 1024-token partitions on 4
+      // waves took 25.3. The 16-bit cache stays on 4 waves: 8 came out
+      // faster only on ragged U[1024, 4096] contexts (bf16 B64 26.2-26.6 ->
+      // 25.8-25.9 us, hd96 22.9-23.1 -> 21.4-21.7) and slower on B64 x 4096
+      // (31.1-31.8 -> 32.2-32.3), B128 x 2048 (32.5-32.7 -> 33.5-33.6), B64 x
+      // U[2048, 4096] and B32 x U[4096, 8192] (26.2-26.5 -> 26.9-27.1).
+      const int64_t wg1024 = units * ((maxctx + 1023) / 1024);
+      if (pl.kv_fp8 && maxctx >= 1024 && wg1024 >= mfma_cu_count() &&
+          wg1024 <= mfma_fixed8_capacity(a->dtype, a->head_dim)) {
+        P = 1024;
+        pl.fixed_waves = 8;
+      }
     }
   } else {
     P = 512;
@@ -999,7 +1017,7 @@ extern "C" int ikl_paged_attention_launch_config(const ikl_paged_attention_args 
   c.path = pl.path;
   c.partition_size = pl.split ? pl.partition : 0;
   if (pl.path == IKL_PATH_MFMA_GROUPED) {
-    const MfmaShape sh = mfma_launch_shape(pl.sk_waves > 0, pl.group_size, pl.sk_unitw);
+    const MfmaShape sh = mfma_launch_shape(pl.sk_waves > 0, pl.group_size, pl.sk_unitw, pl.fixed_waves);
     c.tile_tokens = sh.tile_tokens;
     c.waves_per_workgroup = sh.waves_per_workgroup;
     c.stages = sh.stages;
@@ -1105,6 +1123,7 @@ int run_attention(const ikl_paged_attention_args *a, const Plan &pl, const Fused
   p.sk_waves = pl.sk_waves;
   p.sk_unitw = pl.sk_unitw;
   p.sk_seg_cost = pl.sk_seg_cost;
+  p.fixed_waves = pl.sk_waves > 0 ? 0 : pl.fixed_waves;
   p.units = (int32_t)pl.units;
   p.grid_spread = pl.path == IKL_PATH_MFMA_GROUPED && pl.sk_waves == 0 && spread_grid(pl.units, pl.num_parts, a->batch);
   p.batch = a->batch;

@@ -454,7 +454,7 @@ __device__ __forceinline__ void store_rows_out(const AttnParams &p, int64_t b, i
 
 template <typename Tag, int D, int NG, int WAVES, bool KV8>
 __global__ __launch_bounds__(64 * WAVES) IKL_MFMA_WAVES_ATTR void paged_decode_mfma_kernel(const AttnParams p) {
-  static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4, "1, 2 or 4 waves per workgroup");
+  static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4 || WAVES == 8, "1, 2, 4 or 8 waves per workgroup");
   using WT = WaveTiles<Tag, D, NG, KV8>;
   constexpr int NH = WT::NH;
   // LDS: each wave's V and K tiles during the loop; at the end each wave's
@@ -903,7 +903,10 @@ __global__ __launch_bounds__(64 * UW) __attribute__((amdgpu_waves_per_eu(2, 8)))
 // each wave walked twice the tiles (MQA 32/1 hd128 bf16 step, planned as
 // below: B64 x U[1024, 4096] 27.4 -> 26.3 us, B16 x U[1024, 4096] 16.5 ->
 // 14.6, B64 x 2048 23.9 -> 21.3, over the FP8 cache B64 x U[1024, 4096]
-// 26.9 -> 22.7).
+// 26.9 -> 22.7). Over the FP8 cache the planner can give 32-head units
+// 8-wave workgroups (p.fixed_waves) for 1024-token partitions: 135 KB of LDS
+// at 128 dims, one workgroup and two waves per SIMD on a CU, each wave
+// walking 8 tiles.
 template <int NG>
 constexpr int wg_waves() {
   return 4;
@@ -943,6 +946,12 @@ void launch_shape(const AttnParams &p, dim3 grid, hipStream_t s) {
   }
   // grid arrives as (partition, unit, request)
   grid = p.grid_spread ? dim3(grid.z, grid.y, grid.x) : dim3(grid.y, grid.x, grid.z);
+  if constexpr (NG == 2 && KV8) {
+    if (p.fixed_waves == 8) {
+      paged_decode_mfma_kernel<Tag, D, NG, 8, KV8><<<grid, dim3(512), 0, s>>>(p);
+      return;
+    }
+  }
   constexpr int WAVES = wg_waves<NG>();
   paged_decode_mfma_kernel<Tag, D, NG, WAVES, KV8><<<grid, dim3(64 * WAVES), 0, s>>>(p);
 }
@@ -1017,6 +1026,23 @@ int fixed_capacity_for() {
   return resident_capacity(paged_decode_mfma_kernel<Tag, D, NG, WAVES, KV8>, 64 * WAVES, 8, c);
 }
 
+// The same for the 8-wave form of 32-head units over the FP8 cache.
+template <typename Tag, int D>
+int fixed8_capacity_for() {
+  static std::atomic<int> c[64] = {};
+  return resident_capacity(paged_decode_mfma_kernel<Tag, D, 2, 8, true>, 512, 8, c);
+}
+
+template <typename Tag>
+int fixed8_capacity_dim(int d) {
+  switch (d) {
+    case 32: return fixed8_capacity_for<Tag, 32>();
+    case 64: return fixed8_capacity_for<Tag, 64>();
+    case 96: return fixed8_capacity_for<Tag, 96>();
+    default: return fixed8_capacity_for<Tag, 128>();
+  }
+}
+
 template <typename Tag, int NG, bool KV8>
 int fixed_capacity_dim(int d) {
   switch (d) {
@@ -1062,8 +1088,9 @@ hipError_t launch_mfma_attention(int dtype, int head_dim, const AttnParams &p, d
   return hipGetLastError();
 }
 
-MfmaShape mfma_launch_shape(bool balanced, int group_size, int unitw) {
+MfmaShape mfma_launch_shape(bool balanced, int group_size, int unitw, int fixed_waves) {
   if (balanced && group_size <= 16 && unitw > 1) return MfmaShape{TILE, unitw, 2};
+  if (!balanced && group_size > 16 && fixed_waves == 8) return MfmaShape{TILE, 8, 2};
   const int waves = group_size > 16 ? (balanced ? sk_wg_waves<2>() : wg_waves<2>())
                                     : (balanced ? sk_wg_waves<1>() : wg_waves<1>());
   return MfmaShape{TILE, waves, 2};
@@ -1084,6 +1111,10 @@ int mfma_fixed_capacity(int dtype, int head_dim, int group_size, bool kv_fp8) {
   }
   if (two) return kv_fp8 ? fixed_capacity_dim<f16_tag, 2, true>(head_dim) : fixed_capacity_dim<f16_tag, 2, false>(head_dim);
   return kv_fp8 ? fixed_capacity_dim<f16_tag, 1, true>(head_dim) : fixed_capacity_dim<f16_tag, 1, false>(head_dim);
+}
+
+int mfma_fixed8_capacity(int dtype, int head_dim) {
+  return dtype == IKL_BF16 ? fixed8_capacity_dim<bf16_tag>(head_dim) : fixed8_capacity_dim<f16_tag>(head_dim);
 }
 
 int mfma_cu_count() {

@@ -149,12 +149,22 @@ def test_split_choice_by_batch_size_on_the_mfma_family():
         a = _args(partition_size=0, max_context_len=2048, batch=96, num_kv_heads=1)  # 384
         assert ops.launch_config(a)["split"] == "fixed_partitions"
         # their fixed partitions: the longest of 128-1024 tokens that still
-        # launches a workgroup per CU (two over the FP8 cache)
-        for batch, ctx, want in ((64, 4096, 1024), (16, 4096, 256), (64, 2048, 512), (8, 512, 128)):
-            a = _args(partition_size=0, max_context_len=ctx, batch=batch, num_kv_heads=1)
-            assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == want, (batch, ctx)
+        # launches a workgroup per CU (two over the FP8 cache), on 4-wave
+        # workgroups; over the FP8 cache, 1024-token partitions with a
+        # workgroup per CU, all resident (256 without a device: one 8-wave
+        # group per CU), run on 8 waves instead
+        fp8 = {"cache_dtype": _lib.IKL_FP8_E4M3, "k_scale": 0x60000, "v_scale": 0x70000}
+        for batch, ctx, kw, want, waves in ((64, 4096, {}, 1024, 4), (16, 4096, {}, 256, 4),
+                                            (64, 2048, {}, 512, 4), (8, 512, {}, 128, 4),
+                                            (64, 4096, fp8, 1024, 8), (32, 8192, fp8, 1024, 8),
+                                            (16, 4096, fp8, 128, 4), (64, 2048, fp8, 256, 4)):
+            a = _args(partition_size=0, max_context_len=ctx, batch=batch, num_kv_heads=1, **kw)
+            assert lib.ikl_paged_attention_partition_size(ctypes.byref(a)) == want, (batch, ctx, kw)
             cfg = ops.launch_config(a)
-            assert (cfg["split"], cfg["num_warps"]) == ("fixed_partitions", 4)
+            assert (cfg["split"], cfg["num_warps"]) == ("fixed_partitions", waves), (batch, ctx, kw)
+        # an explicit partition size keeps 4-wave workgroups
+        a = _args(partition_size=1024, max_context_len=4096, batch=64, num_kv_heads=1, **fp8)
+        assert ops.launch_config(a)["num_warps"] == 4
     # -2: the balanced split on a small batch too
     a = _args(partition_size=-2, max_context_len=1024, batch=2)
     part = lib.ikl_paged_attention_partition_size(ctypes.byref(a))

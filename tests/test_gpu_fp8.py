@@ -118,6 +118,34 @@ def test_fp8_decode_attention_matches_oracle(act, heads, kv, dim, bs, lengths, p
     assert max_abs_err(out, _expected(base), act) < ATOL[act]
 
 
+@pytest.mark.parametrize("act,dim", [("bfloat16", 128), ("float16", 128), ("bfloat16", 96), ("float16", 64)])
+def test_fp8_cache_8_wave_fixed_partitions(act, dim):
+    """MQA 32/1 over the FP8 cache, 64 requests, longest context 4096:
+    1024-token partitions on 8-wave workgroups (in place of 512-token ones
+    at two 4-wave workgroups per CU). The other lengths are short and ragged
+    (one token, a tile and one token, a partition and one token), which
+    leaves waves without tiles and partitions part-filled, and keeps the
+    oracle cheap."""
+    from inferkernellab_amd import ops
+
+    gen = np.random.default_rng(93 + dim)
+    lengths = [int(x) for x in gen.integers(1, 600, size=64)]
+    lengths[:5] = [4096, 1, 17, 1025, 2049]
+    base, packed = _fp8_case(batch=64, heads=32, kv=1, dim=dim, bs=16, lengths=lengths, act=act, seed=94)
+    cache = _device_fp8_cache(base, packed, act)
+    print(f"fp8 8-wave case act={act} D={dim} lens={lengths[:8]}", flush=True)
+    attn = ops.PreparedPagedAttention(base.device_query(), cache, base.device_tables(), base.device_lengths(),
+                                      max_context_len=max(lengths))
+    launch = attn.launch
+    assert (launch["path"], launch["split"], launch["partition_size"], launch["num_warps"]) == \
+        ("mfma_grouped", "fixed_partitions", 1024, 8)
+    got = attn()
+    torch.cuda.synchronize()
+    out = got.float().cpu().numpy()
+    assert not np.isnan(out).any()
+    assert max_abs_err(out, _expected(base), act) < ATOL[act]
+
+
 def test_fp8_append_then_attention_and_quantisation_error():
     """New tokens quantised by the HIP append, then attended: equal to the
     oracle on the dequantised cache; the FP8 error against the same
